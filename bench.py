@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Tree-verification attention benchmark on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+A step is one ragged verify attention call (``varlen_tree_attention``) over
+the Qwen3-8B-shaped workload B=8 requests x (prefix 8192 + tree of 128
+packed tokens), 32 query / 8 KV heads, head_dim 128, bf16, inputs resident
+in HBM.  K/V come from rotating buffer sets (3 x 273 MB) so the 256 MB
+Infinity Cache cannot serve a call's keys from the previous call.  Each call
+is bracketed by HIP events on the launch stream: attention kernel, split-K
+combine.  One JSON line goes to stdout; progress goes to stderr.
+
+Also reported: the roofline of the attention kernel (binding side from the
+algorithmic bytes and flops), the HBM fraction the metric names, the CPU
+oracle timed on host cores on a one-request sample, and secondary workloads
+(bitmask and greedy-accept kernels, the other benchmark shapes).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "tree-verify attn µs/call + % HBM roofline, Qwen3-8B shape, N=128, ctx 8k, B=8"
+PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
+PEAK_MFMA_BF16 = 2.5e15    # FLOP/s, dense bf16
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roofline(wl, seconds):
+    """Binding-side roofline of one attention call over ``wl``."""
+    byt, flo = wl.algorithmic_bytes(), wl.algorithmic_flops()
+    t_hbm, t_mfma = byt / PEAK_HBM, flo / PEAK_MFMA_BF16
+    if t_mfma >= t_hbm:
+        ach = flo / seconds / 1e12
+        return dict(bound="mfma", achieved=round(ach, 2), peak=PEAK_MFMA_BF16 / 1e12, unit="TFLOP/s",
+                    frac=round(ach / (PEAK_MFMA_BF16 / 1e12), 4))
+    ach = byt / seconds / 1e9
+    return dict(bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM / 1e9, unit="GB/s",
+                frac=round(ach / (PEAK_HBM / 1e9), 4))
+
+
+class Harness:
+    """Resident inputs of one workload, with rotated K/V sets."""
+
+    def __init__(self, wl, dev, sets, kv_split):
+        import numpy as np
+        import torch
+        from cast_amd import tree_bitmask
+        self.wl, self.dev, self.kv_split = wl, dev, kv_split
+        self.meta = wl.meta_tensors(dev)
+        self.mask = tree_bitmask(self.meta["parent"], self.meta["cu_q"], 2)
+        self.sets = []
+        for s in range(sets):
+            wl.seed = 1000 + s
+            self.sets.append(wl.qkv(device=dev, generator_device=dev))
+        wl.seed = 0
+        self.out = torch.empty_like(self.sets[0][0])
+        from cast_amd.tree_attn import plan
+        p = plan(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, kv_split=kv_split)
+        self.plan = p
+        self.ws = torch.empty(max(p.workspace_bytes, 256), dtype=torch.uint8, device=dev)
+        del np
+
+    def call(self, i, hook=None):
+        from cast_amd import varlen_tree_attention
+        q, k, v = self.sets[i % len(self.sets)]
+        m = self.meta
+        return varlen_tree_attention(q, k, v, m["cu_q"], m["cu_kv"], m["prefix_len"], m["pack_len"], self.mask,
+                                     return_lse=True, kv_split=self.kv_split, out=self.out, workspace=self.ws,
+                                     _stage_hook=hook)
+
+    def time(self, steps, warmup):
+        import torch
+        for i in range(warmup):
+            self.call(i)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            self.call(i, hook=lambda s, e=ev[i]: e[s].record())
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        attn = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]     # us
+        comb = [e[1].elapsed_time(e[2]) * 1e3 for e in ev]
+        call = [e[0].elapsed_time(e[2]) * 1e3 for e in ev]
+        return dict(call_us=statistics.median(call), call_mean_us=statistics.fmean(call),
+                    attn_us=statistics.median(attn), attn_mean_us=statistics.fmean(attn),
+                    combine_us=statistics.median(comb), wall_us=wall / steps * 1e6)
+
+
+def time_kernel(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        ev[i][0].record()
+        fn()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return statistics.median(e[0].elapsed_time(e[1]) * 1e3 for e in ev)
+
+
+def cpu_baseline(wl, budget_s=12.0):
+    """The oracle (dense fp32 torch on host cores) on request 0, scaled to B."""
+    import torch
+    from oracle import attn as oracle_attn
+    from oracle import bitmask as oracle_bitmask
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, k, v = wl.qkv(device="cpu")
+    words = oracle_bitmask.chain_walk_words(wl.packed.parent, wl.cu_q)
+    qf, kf, vf = q.float(), k.float(), v.float()
+
+    def run():
+        oracle_attn.dense_tree_attention(qf, kf, vf, wl.cu_q, wl.cu_kv, wl.prefix_len, wl.pack_len, words,
+                                         requests=[0])
+
+    run()
+    times, t_end = [], time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 30):
+        t = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    S0, P0 = int(wl.prefix_len[0]), int(wl.pack_len[0])
+    return dict(value=round(med * wl.B * 1e6, 1), unit="us/call", cores=cores, kind="port",
+                sample=f"request 0 of {wl.B} (S={S0}, P={P0}, {wl.Hq}/{wl.Hkv} heads, D={wl.D}): dense fp32 "
+                       f"torch oracle on the bf16-rounded inputs, median of {len(times)} runs "
+                       f"({med * 1e3:.1f} ms each), scaled x{wl.B}")
+
+
+def secondary(dev, steps, warmup):
+    import torch
+    from cast_amd import greedy_accept, scenarios, tree_bitmask
+    res = {}
+    for name in ("qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128", "qwen3-8b-stress-b32"):
+        wl = scenarios.CONFIGS[name]()
+        h = Harness(wl, dev, sets=2, kv_split=0)
+        t = h.time(steps, warmup)
+        rl = roofline(wl, t["attn_us"] * 1e-6)
+        res[name] = dict(us_per_call=round(t["call_us"], 2), attn_us=round(t["attn_us"], 2),
+                         combine_us=round(t["combine_us"], 2), bound=rl["bound"], frac=rl["frac"],
+                         hbm_frac=round(wl.algorithmic_bytes() / (t["call_us"] * 1e-6) / PEAK_HBM, 4),
+                         tokens=int(wl.total_q), kv_tokens=int(wl.total_kv))
+        log(f"  {name}: {t['call_us']:.1f} us/call (attn {t['attn_us']:.1f}, combine {t['combine_us']:.1f}), "
+            f"{rl['bound']} frac {rl['frac']:.3f}")
+        del h
+        torch.cuda.empty_cache()
+    # K1 and K3 on the headline trees, full Qwen3 vocabulary logits
+    wl = scenarios.qwen3_headline()
+    meta = wl.meta_tensors(dev)
+    t_bm = time_kernel(lambda: tree_bitmask(meta["parent"], meta["cu_q"], 2), steps, warmup)
+    g = torch.Generator(device=dev).manual_seed(0)
+    logits = torch.randn(wl.total_q, wl.vocab, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    tok = torch.from_numpy(wl.packed.token).to(dev)
+    t_acc = time_kernel(lambda: greedy_accept(logits, meta["cu_q"], meta["parent"], tok), steps, warmup)
+    lb = wl.total_q * wl.vocab * 2
+    res["tree_bitmask"] = dict(us_per_call=round(t_bm, 2), rows=int(wl.total_q))
+    res["greedy_accept"] = dict(us_per_call=round(t_acc, 2), logits_bytes=lb,
+                                hbm_frac=round(lb / (t_acc * 1e-6) / PEAK_HBM, 4))
+    log(f"  tree_bitmask {t_bm:.1f} us, greedy_accept {t_acc:.1f} us ({lb / t_acc / 1e3:.0f} GB/s)")
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sets", type=int, default=3, help="rotated K/V buffer sets")
+    ap.add_argument("--kv-split", type=int, default=0, help="keys per split-K chunk (0: library choice)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the verify path shards by request and KV head with no exchange, so no multi-GPU figure "
+              "is produced", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from cast_amd import scenarios
+    dev = torch.device("cuda:0")
+    log(f"device: {torch.cuda.get_device_name(dev)}")
+    wl = scenarios.qwen3_headline()
+    h = Harness(wl, dev, sets=args.sets, kv_split=args.kv_split)
+    log(f"workload {wl.name}: total_q={wl.total_q} total_kv={wl.total_kv} kv_split={h.plan.kv_split} "
+        f"workspace={h.plan.workspace_bytes / 2**20:.1f} MiB")
+    t = h.time(args.steps, args.warmup)
+    log(f"  call {t['call_us']:.1f} us (mean {t['call_mean_us']:.1f}), attention kernel {t['attn_us']:.1f} us, "
+        f"combine {t['combine_us']:.1f} us, host wall {t['wall_us']:.1f} us/call")
+    rl = roofline(wl, t["attn_us"] * 1e-6)
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get(wl.name, {}).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    rl["traffic"] = traffic
+    call_s = t["call_us"] * 1e-6
+    line = {
+        "metric": METRIC, "value": round(t["call_us"], 2), "unit": "us/call", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t["call_us"] / 1e3, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian Q/K/V, trees from seeded N(0,5) 15x151936 block scores)",
+        "config": {"workload": wl.name, "batch": wl.B, "prefix": int(wl.prefix_len[0]),
+                   "pack": int(wl.pack_len[0]), "q_heads": wl.Hq, "kv_heads": wl.Hkv, "head_dim": wl.D,
+                   "kv_split": h.plan.kv_split, "kv_sets": args.sets},
+        "roofline": rl,
+        "hbm_frac": round(wl.algorithmic_bytes() / call_s / PEAK_HBM, 4),
+        "tokens_per_s": round(wl.total_q / call_s, 1),
+        "attn_kernel_us": round(t["attn_us"], 2), "combine_us": round(t["combine_us"], 2),
+        "call_mean_us": round(t["call_mean_us"], 2), "host_wall_us": round(t["wall_us"], 2),
+        "algorithmic_bytes": wl.algorithmic_bytes(), "algorithmic_flops": wl.algorithmic_flops(),
+    }
+    del h
+    torch.cuda.empty_cache()
+    if not args.no_secondary:
+        log("secondary workloads:")
+        line["secondary"] = secondary(dev, max(10, args.steps // 3), max(3, args.warmup // 3))
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle on host cores)...")
+        line["cpu_baseline"] = cpu_baseline(wl)
+        log(f"  {line['cpu_baseline']}")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,109 @@
+"""ctypes binding of libcast_amd.so (the C ABI declared in include/cast_amd.h).
+
+There is no fallback: if the library is missing, every device entry point
+raises.  ``torch`` is imported before the library is opened so that the
+process maps torch's HIP runtime and the library binds to the same one.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libcast_amd.so")
+
+OK = 0
+ERR_HEAD_RATIO = 2
+ERR_PACK_TOO_LARGE = 3
+ERR_HIP = 10
+
+FLAG_BAD_PACK = 1
+FLAG_BAD_OFFSETS = 2
+FLAG_BAD_PARENT = 4
+
+BF16, FP32 = 0, 1
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+_ATTN_ARGS = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+              _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, ctypes.c_float, _I32, _P, _SZ, _P, _P]
+
+SIGNATURES = {
+    "cast_abi_version": ([], ctypes.c_int),
+    "cast_status_string": ([ctypes.c_int], ctypes.c_char_p),
+    "cast_tree_bitmask": ([_P, _P, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
+    "cast_tree_attn_fwd": (_ATTN_ARGS, ctypes.c_int),
+    "cast_tree_attn_partial": (_ATTN_ARGS, ctypes.c_int),
+    "cast_tree_attn_combine": (_ATTN_ARGS, ctypes.c_int),
+    "cast_tree_attn_workspace_size": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32], _SZ),
+    "cast_tree_attn_default_split": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32], _I32),
+    "cast_greedy_accept": ([_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P], ctypes.c_int),
+}
+
+_lib = None
+
+
+class CastError(RuntimeError):
+    """A C-ABI call returned an error status."""
+
+    def __init__(self, status, what):
+        self.status = status
+        super().__init__(f"{what}: {status_string(status)} (status {status})")
+
+
+def load():
+    """Open the library once; raise if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m cast_amd.build` "
+                           "(the HIP path has no CPU fallback)")
+    import torch  # noqa: F401  (map torch's libamdhip64 first)
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def status_string(status):
+    try:
+        return load().cast_status_string(int(status)).decode()
+    except Exception:
+        return "unknown status"
+
+
+def check(status, what):
+    if status != OK:
+        if status == ERR_HEAD_RATIO:
+            raise AssertionError(f"{what}: query heads must be a multiple of KV heads")
+        raise CastError(status, what)
+
+
+def stream_of(tensor):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+
+
+def ptr(tensor):
+    return ctypes.c_void_p(tensor.data_ptr()) if tensor is not None else ctypes.c_void_p(0)
+
+
+def raise_device_flags(flags, what):
+    """Turn the device status word into an exception (after a sync)."""
+    flags = int(flags)
+    if not flags:
+        return
+    parts = []
+    if flags & FLAG_BAD_PACK:
+        parts.append("a pack is empty or longer than the mask words allow (128 tokens, 64 with one word)")
+    if flags & FLAG_BAD_OFFSETS:
+        parts.append("cu_q / cu_kv / prefix_len / pack_len are inconsistent")
+    if flags & FLAG_BAD_PARENT:
+        parts.append("a parent index is not in [-1, own index)")
+    raise ValueError(f"{what}: " + "; ".join(parts))

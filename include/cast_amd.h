@@ -1,0 +1,169 @@
+/*
+ * cast_amd.h - C ABI of the MI355X (gfx950) tree-verification library.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is device memory
+ * unless stated otherwise; every entry point is stream-ordered on the
+ * hipStream_t passed as `stream` (NULL = the null stream), performs no host
+ * synchronisation and allocates nothing: scratch memory is passed in by the
+ * caller.  Entry points validate their host-side arguments before touching
+ * the GPU and return a cast_status code; metadata that lives on the device
+ * (pack lengths, offsets, parents) is checked by the kernels, which skip the
+ * offending request and raise a bit in the optional device status word.
+ *
+ * Packed layout (cast_trees/serving.py:211-231): request b owns query rows
+ * [cu_q[b], cu_q[b+1]) = its pack (root + tree nodes, P_b = pack_len[b] <= 128
+ * tokens) and key/value rows [cu_kv[b], cu_kv[b+1]) = concat(prefix of
+ * S_b = prefix_len[b] tokens, pack).  Bit j of a row's ancestor words marks
+ * pack-local key j visible; word w holds bits 64w..64w+63.
+ */
+#ifndef CAST_AMD_H
+#define CAST_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *cast_stream_t; /* a hipStream_t */
+
+enum cast_status {
+    CAST_OK = 0,
+    CAST_ERR_NULL_POINTER = 1,     /* a required pointer is NULL */
+    CAST_ERR_HEAD_RATIO = 2,       /* query heads not a multiple of KV heads */
+    CAST_ERR_PACK_TOO_LARGE = 3,   /* a pack bound above 128 tokens (or 64 with one word) */
+    CAST_ERR_DTYPE = 4,            /* unsupported element type */
+    CAST_ERR_HEAD_DIM = 5,         /* unsupported head dimension */
+    CAST_ERR_ALIGNMENT = 6,        /* pointer or stride breaks the 16-byte rule */
+    CAST_ERR_SHAPE = 7,            /* negative or inconsistent sizes */
+    CAST_ERR_WORKSPACE = 8,        /* workspace smaller than the queried size */
+    CAST_ERR_SCALE = 9,            /* softmax scale not finite and positive */
+    CAST_ERR_HIP = 10              /* a HIP runtime call or launch failed */
+};
+
+/* Bits a kernel ORs into the optional device status word (int32). */
+enum cast_device_flag {
+    CAST_FLAG_BAD_PACK = 1,        /* pack_len outside [1, 128] or beyond the mask words */
+    CAST_FLAG_BAD_OFFSETS = 2,     /* cu_q / cu_kv / prefix_len inconsistent with totals */
+    CAST_FLAG_BAD_PARENT = 4       /* a parent index not in [-1, own index) */
+};
+
+enum cast_dtype { CAST_BF16 = 0, CAST_FP32 = 1 };
+
+/* Library ABI version (bumped on any signature change). */
+int cast_abi_version(void);
+
+/* Human-readable text of a cast_status code. */
+const char *cast_status_string(int status);
+
+/* ---------------------------------------------------------------------
+ * K1: packed ancestor bitmask.
+ * Replaces the host loop of cast_trees/serving.py:213-222 (and the dense
+ * cast_trees/tree.py:85-93 ancestor_matrix it encodes).
+ *   parent     int32 [total_q]  pack-local parent of every packed row, -1 at
+ *                               each pack's root (row 0 of the pack)
+ *   cu_q       int32 [batch+1]  pack offsets
+ *   words_out  uint64 [total_q][words_per_row]; words_per_row 1 gives the
+ *                               reference's int64 word (packs <= 64 tokens),
+ *                               2 covers packs <= 128 tokens
+ *   status     int32*, nullable device status word (cast_device_flag bits)
+ * ------------------------------------------------------------------- */
+int cast_tree_bitmask(const int32_t *parent, const int32_t *cu_q, int32_t batch,
+                      int32_t total_q, int32_t words_per_row, uint64_t *words_out,
+                      int32_t *status, cast_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * K2: ragged ancestor-masked tree-verification attention (forward).
+ * Replaces the tile schedule and kernel launch of
+ * cast_trees/tree_attn.py:116-139 (kernel body tree_attn.py:17-92).
+ *   q      [total_q,  Hq,  D]  strides (q_tok, q_head, 1), in elements
+ *   k, v   [total_kv, Hkv, D]  strides (k_tok, k_head, 1) / (v_tok, v_head, 1)
+ *   out    [total_q,  Hq,  D]  strides (o_tok, o_head, 1), same dtype as q
+ *   lse    float [total_q, Hq] contiguous, natural-log log-sum-exp of the
+ *                              scaled scores over visible keys; nullable
+ *   cu_q, cu_kv  int32 [batch+1];  prefix_len, pack_len  int32 [batch]
+ *   mask   uint64 [total_q][mask_words], mask_words 1 (int64 reference
+ *          layout) or 2
+ *   dtype  cast_dtype of q, k, v and out
+ *   sm_scale  > 0 (the Python layer substitutes 1/sqrt(D) for None)
+ *   kv_split  keys per split-K chunk (multiple of 64); 0 lets the library
+ *             choose from the shapes; a negative value disables split-K
+ *   workspace / workspace_bytes  scratch of at least
+ *             cast_tree_attn_workspace_size(...) bytes, 256-byte aligned
+ *   status    int32*, nullable device status word
+ * Rows with no visible key produce zeros and lse = -inf.
+ * ------------------------------------------------------------------- */
+int cast_tree_attn_fwd(const void *q, const void *k, const void *v, void *out, float *lse,
+                       const int32_t *cu_q, const int32_t *cu_kv, const int32_t *prefix_len,
+                       const int32_t *pack_len, const uint64_t *mask, int32_t mask_words,
+                       int32_t batch, int32_t total_q, int32_t total_kv, int32_t num_q_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
+                       int64_t k_tok, int64_t k_head, int64_t v_tok, int64_t v_head,
+                       int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,
+                       int32_t kv_split, void *workspace, size_t workspace_bytes,
+                       int32_t *status, cast_stream_t stream);
+
+/* The two stages of cast_tree_attn_fwd, same arguments, for callers that
+ * interleave other work or time the stages separately:
+ *   _partial  the attention kernel; requests that are split over keys leave
+ *             their rows of out/lse unwritten and their partials in workspace
+ *   _combine  merges those partials into out/lse (a no-op without split-K)
+ * Same-stream order partial -> combine equals cast_tree_attn_fwd.  Both
+ * replace the same reference launch (cast_trees/tree_attn.py:128-138). */
+int cast_tree_attn_partial(const void *q, const void *k, const void *v, void *out, float *lse,
+                           const int32_t *cu_q, const int32_t *cu_kv, const int32_t *prefix_len,
+                           const int32_t *pack_len, const uint64_t *mask, int32_t mask_words,
+                           int32_t batch, int32_t total_q, int32_t total_kv, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
+                           int64_t k_tok, int64_t k_head, int64_t v_tok, int64_t v_head,
+                           int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,
+                           int32_t kv_split, void *workspace, size_t workspace_bytes,
+                           int32_t *status, cast_stream_t stream);
+int cast_tree_attn_combine(const void *q, const void *k, const void *v, void *out, float *lse,
+                           const int32_t *cu_q, const int32_t *cu_kv, const int32_t *prefix_len,
+                           const int32_t *pack_len, const uint64_t *mask, int32_t mask_words,
+                           int32_t batch, int32_t total_q, int32_t total_kv, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
+                           int64_t k_tok, int64_t k_head, int64_t v_tok, int64_t v_head,
+                           int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,
+                           int32_t kv_split, void *workspace, size_t workspace_bytes,
+                           int32_t *status, cast_stream_t stream);
+
+/* Workspace bytes cast_tree_attn_fwd needs for these host-known sizes. */
+size_t cast_tree_attn_workspace_size(int32_t batch, int32_t total_q, int32_t total_kv,
+                                     int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t dtype, int32_t kv_split);
+
+/* The split-K chunk (keys) the library would choose for kv_split = 0. */
+int32_t cast_tree_attn_default_split(int32_t batch, int32_t total_q, int32_t total_kv,
+                                     int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t dtype);
+
+/* ---------------------------------------------------------------------
+ * K3: greedy accepted-path walk over verify logits, no host sync.
+ * Replaces the temperature-0 walk of cast_trees/decode.py:85-103 (pick at
+ * decode.py:13-15) called per request at cast_trees/serving.py:326-335.
+ *   logits   [total_q, vocab], row stride logits_ld elements, dtype
+ *            CAST_BF16 or CAST_FP32; packed row r = pack row (root first)
+ *   cu_q     int32 [batch+1];  parent int32 [total_q] pack-local (-1 root)
+ *   token    int64 [total_q]  draft token of every packed row (root ignored)
+ *   argmax   int32 [total_q]  out: first index of each row's maximum
+ *            (NaN counts as the maximum, as torch.argmax)
+ *   path     int32 [batch][128] out: accepted node indices (pack index - 1),
+ *            root-to-leaf, -1 padded
+ *   path_len int32 [batch] out: accepted nodes per request
+ *   bonus    int64 [batch] out: the target's token after the accepted path
+ *   status   int32*, nullable device status word
+ * ------------------------------------------------------------------- */
+int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t vocab, int32_t dtype,
+                       const int32_t *cu_q, const int32_t *parent, const int64_t *token,
+                       int32_t batch, int32_t total_q, int32_t *argmax, int32_t *path,
+                       int32_t *path_len, int64_t *bonus, int32_t *status,
+                       cast_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CAST_AMD_H */

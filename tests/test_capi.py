@@ -1,0 +1,90 @@
+"""The C ABI: the library loads, exports every declared symbol, and rejects
+bad host-side arguments before touching the GPU (no GPU needed)."""
+import re
+from pathlib import Path
+
+import pytest
+
+from cast_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "cast_amd.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(cast_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libcast_amd.so is not built (run `python -m cast_amd.build` or __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared()
+    assert names == sorted(_lib.SIGNATURES), "ctypes bindings and header disagree"
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.cast_abi_version() == 1
+
+
+def test_status_strings(lib):
+    for code in range(11):
+        assert lib.cast_status_string(code)
+    assert b"multiple of KV heads" in lib.cast_status_string(2)
+
+
+def _attn(lib, **over):
+    args = dict(q=None, k=None, v=None, out=None, lse=None, cu_q=None, cu_kv=None, prefix=None, pack=None,
+                mask=None, words=2, B=1, tq=16, tkv=32, Hq=32, Hkv=8, D=128, strides=[0] * 8, dtype=0,
+                scale=0.1, split=0, ws=None, wsb=0, status=None, stream=None)
+    args.update(over)
+    a = args
+    return lib.cast_tree_attn_fwd(a["q"], a["k"], a["v"], a["out"], a["lse"], a["cu_q"], a["cu_kv"], a["prefix"],
+                                  a["pack"], a["mask"], a["words"], a["B"], a["tq"], a["tkv"], a["Hq"], a["Hkv"],
+                                  a["D"], *a["strides"], a["dtype"], a["scale"], a["split"], a["ws"], a["wsb"],
+                                  a["status"], a["stream"])
+
+
+def test_attention_host_validation(lib):
+    assert _attn(lib, Hq=32, Hkv=7) == 2                 # head ratio
+    assert _attn(lib, Hkv=0) == 2
+    assert _attn(lib, dtype=5) == 4                      # dtype
+    assert _attn(lib, words=3) == 7                      # mask words
+    assert _attn(lib, scale=0.0) == 9                    # scale
+    assert _attn(lib, scale=float("nan")) == 9
+    assert _attn(lib, B=-1) == 7
+    assert _attn(lib) == 1                               # null pointers
+    assert _attn(lib, B=0) == 0 and _attn(lib, tq=0) == 0  # nothing to do
+
+
+def test_workspace_and_split_are_host_only(lib):
+    # the headline shape: 8 requests x (8192 prefix + 128 pack), Qwen3 heads
+    split = lib.cast_tree_attn_default_split(8, 1024, 66560, 32, 8, 128, 0)
+    assert split > 0 and split % 64 == 0
+    ws = lib.cast_tree_attn_workspace_size(8, 1024, 66560, 32, 8, 128, 0, 0)
+    assert ws > 0 and ws % 256 == 0
+    assert lib.cast_tree_attn_workspace_size(8, 1024, 66560, 32, 8, 128, 0, -1) == 0     # no split
+    assert lib.cast_tree_attn_workspace_size(1, 16, 144, 4, 4, 64, 1, 0) == 0            # fp32 path
+    assert lib.cast_tree_attn_workspace_size(8, 1024, 66560, 32, 7, 128, 0, 0) == 0      # bad ratio
+
+
+def test_bitmask_and_accept_validation(lib):
+    assert lib.cast_tree_bitmask(None, None, 1, 1, 3, None, None, None) == 7
+    assert lib.cast_tree_bitmask(None, None, 1, 4, 2, None, None, None) == 1
+    assert lib.cast_tree_bitmask(None, None, 0, 0, 2, None, None, None) == 0
+    assert lib.cast_greedy_accept(None, 10, 10, 0, None, None, None, 1, 1, None, None, None, None, None, None) == 1
+    assert lib.cast_greedy_accept(None, 5, 10, 0, None, None, None, 1, 1, None, None, None, None, None, None) == 7
+    assert lib.cast_greedy_accept(None, 10, 10, 9, None, None, None, 1, 1, None, None, None, None, None, None) == 4
+
+
+def test_python_layer_maps_errors():
+    with pytest.raises(AssertionError):
+        _lib.check(2, "x")
+    with pytest.raises(_lib.CastError):
+        _lib.check(10, "x")
+    with pytest.raises(ValueError):
+        _lib.raise_device_flags(_lib.FLAG_BAD_PARENT, "x")
+    _lib.raise_device_flags(0, "x")

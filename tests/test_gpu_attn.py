@@ -1,0 +1,140 @@
+"""Tree attention on the GPU (through the C ABI) vs the dense CPU oracle.
+
+Bar: fp32-accumulated bf16 outputs within max-abs 2e-2 of the fp32 oracle on
+the same (bf16-rounded) inputs, natural-log LSE within 1e-3; fp32 inputs
+within 1e-4 / 1e-4.  The reference's own kernel test uses
+max < 5e-2, mean < 5e-3 (tests/test_tree_attn.py:74); these bounds are tighter.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cast_amd import scenarios as SC
+from oracle import attn as OA
+from oracle import bitmask as OB
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": dict(out=2e-2, lse=1e-3, mean=2e-3), "fp32": dict(out=1e-4, lse=1e-4, mean=1e-5)}
+
+
+def _words(wl):
+    return OB.chain_walk_words(wl.packed.parent, wl.cu_q)
+
+
+def _run_and_check(wl, dev, requests=None, kv_heads=None, kv_split=0, one_word=False, q_noncontig=False,
+                   label=""):
+    from cast_amd import varlen_tree_attention
+    print(f"case {label or wl.name}: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv} "
+          f"Hq={wl.Hq} Hkv={wl.Hkv} D={wl.D} {wl.dtype} split={kv_split}", flush=True)
+    q, k, v = wl.qkv(device=dev)
+    words = _words(wl)
+    if one_word:
+        assert not words[:, 1].any()
+        mask_dev = torch.from_numpy(words[:, 0].view(np.int64).copy()).to(dev)
+    else:
+        mask_dev = torch.from_numpy(words.view(np.int64).copy()).to(dev)
+    meta = wl.meta_tensors(dev)
+    if q_noncontig:
+        # the serving hook hands over query[0].transpose(0, 1): head-major storage
+        q = q.transpose(0, 1).contiguous().transpose(0, 1)
+    out, lse = varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                                     mask_dev, return_lse=True, kv_split=kv_split, check=True)
+    torch.cuda.synchronize()
+    ref_o, ref_l = OA.dense_tree_attention(q.float().cpu(), k.float().cpu(), v.float().cpu(), wl.cu_q, wl.cu_kv,
+                                           wl.prefix_len, wl.pack_len, words, requests=requests,
+                                           kv_heads=kv_heads)
+    sel = ~torch.isnan(ref_l)
+    got_o, got_l = out.float().cpu(), lse.cpu()
+    err_o = (got_o - ref_o).abs()[sel]
+    err_l = (got_l - ref_l).abs()[sel & torch.isfinite(ref_l)]
+    tol = TOL[wl.dtype]
+    print(f"  out max {err_o.max():.3e} mean {err_o.mean():.3e}  lse max {err_l.max():.3e}", flush=True)
+    assert torch.isfinite(got_o[sel]).all()
+    assert err_o.max() <= tol["out"] and err_o.mean() <= tol["mean"]
+    assert err_l.max() <= tol["lse"]
+    assert torch.equal(torch.isneginf(got_l[sel]), torch.isneginf(ref_l[sel]))
+    return out, lse
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_reference_scenario(gpu, dtype):
+    # the reference kernel test's batch: B=8, S~U[200,400), P~U[2,64), random parents
+    wl = SC.random_parent_batch(seed=0, dtype=dtype)
+    _run_and_check(wl, gpu, label=f"reference-scenario-{dtype}")
+    _run_and_check(wl, gpu, one_word=True, label=f"reference-scenario-{dtype}-int64-mask")
+
+
+def test_cpu_plumbing_config(gpu):
+    _run_and_check(SC.cpu_plumbing(), gpu)
+
+
+def test_qwen3_single(gpu):
+    _run_and_check(SC.qwen3_single(), gpu)
+    _run_and_check(SC.qwen3_single(), gpu, kv_split=-1, label="qwen3-single-nosplit")
+    _run_and_check(SC.qwen3_single(), gpu, q_noncontig=True, label="qwen3-single-headmajor-q")
+
+
+def test_qwen3_ragged_full_oracle(gpu):
+    _run_and_check(SC.qwen3_ragged(seed=0), gpu)
+
+
+@pytest.mark.parametrize("split", [64, 256, 1000, -1])
+def test_split_k_variants_agree(gpu, split):
+    wl = SC.qwen3_ragged(seed=3, B=4, lo=100, hi=3000)
+    _run_and_check(wl, gpu, kv_split=split, label=f"ragged-split{split}")
+
+
+def test_edge_packs(gpu):
+    # S=0 pure tree, P=1 root only, P=128 chain, P=128 star, S not a multiple of 32
+    from cast_amd.tree import TreeNode
+    chain = [TreeNode(i, i + 1, i - 1, 0.0) for i in range(127)]
+    star = [TreeNode(i, 1, -1, 0.0) for i in range(127)]
+    wl = SC._make("edges", [chain, [], star, chain[:5], star[:63]], [0, 77, 1, 4099, 33],
+                  SC.QWEN3_8B, "bf16", 5, 1 / math.sqrt(128))
+    _run_and_check(wl, gpu)
+    _run_and_check(wl, gpu, kv_split=64, label="edges-split64")
+
+
+def test_gqa_ratios_and_head_dim_64(gpu):
+    for Hq, Hkv, D, dt in [(8, 8, 64, "bf16"), (16, 2, 64, "bf16"), (64, 8, 128, "bf16"), (12, 4, 96, "bf16"),
+                           (8, 2, 128, "fp32")]:
+        wl = SC.random_parent_batch(seed=Hq + D, B=3, Hq=Hq, Hkv=Hkv, D=D, s_lo=50, s_hi=700, p_lo=1, p_hi=129,
+                                    dtype=dt, qkv_scale=0.5)
+        _run_and_check(wl, gpu, label=f"gqa{Hq}/{Hkv}-D{D}-{dt}")
+
+
+def test_empty_rows_give_zero_and_minus_inf(gpu):
+    from cast_amd import varlen_tree_attention
+    wl = SC.random_parent_batch(seed=9, B=2, Hq=8, Hkv=2, D=128, s_lo=0, s_hi=1, p_lo=5, p_hi=6, dtype="bf16")
+    q, k, v = wl.qkv(device=gpu)
+    words = _words(wl)
+    words[1] = 0                          # row 1 sees nothing (S = 0)
+    meta = wl.meta_tensors(gpu)
+    out, lse = varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                                     torch.from_numpy(words.view(np.int64).copy()).to(gpu), return_lse=True)
+    assert torch.all(out[1] == 0) and torch.all(torch.isneginf(lse[1]))
+    assert torch.isfinite(lse[0]).all()
+
+
+def test_large_configs_sampled(gpu):
+    # full-size inputs, oracle on a sample of (request, KV head) pairs
+    for wl, reqs in [(SC.qwen3_headline(), [0, 5]), (SC.llama_long(), [0]), (SC.stress_mixed(), [0, 1, 30])]:
+        _run_and_check(wl, gpu, requests=reqs, kv_heads=[0, 7], label=wl.name)
+
+
+def test_metadata_errors_are_flagged_not_faulted(gpu):
+    from cast_amd import varlen_tree_attention
+    wl = SC.random_parent_batch(seed=2, B=2, Hq=8, Hkv=2, D=128, s_lo=10, s_hi=20, p_lo=4, p_hi=8, dtype="bf16")
+    q, k, v = wl.qkv(device=gpu)
+    meta = wl.meta_tensors(gpu)
+    mask = torch.from_numpy(_words(wl).view(np.int64).copy()).to(gpu)
+    bad = meta["pack_len"].clone()
+    bad[0] += 1                           # disagrees with cu_q
+    with pytest.raises(ValueError):
+        varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], bad, mask, check=True)
+    with pytest.raises(AssertionError):
+        varlen_tree_attention(q, k[:, :1].expand(-1, 3, -1), v[:, :1].expand(-1, 3, -1), meta["cu_q"],
+                              meta["cu_kv"], meta["prefix_len"], meta["pack_len"], mask)
