@@ -46,10 +46,13 @@ __global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict_
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
             float v;
+            // copy the lane element to a scalar first: a bit cast of a
+            // vector element expression reads the vector's first element
+            const uint32_t bits = w[BF16 ? (e >> 1) : e];
             if constexpr (BF16)
-                v = bf16_to_float((uint16_t)(w[e >> 1] >> ((e & 1) * 16)));
+                v = bf16_to_float((uint16_t)(bits >> ((e & 1) * 16)));
             else
-                v = __builtin_bit_cast(float, w[e]);
+                v = __builtin_bit_cast(float, bits);
             const int i = c * EPC + e;
             if (better(v, i, best, bi)) {
                 best = v;
