@@ -112,25 +112,44 @@ __device__ __forceinline__ bool pack_bit(int j, uint64_t w0, uint64_t w1) {
 }
 
 // --------------------------------------------------------------------------
-// MFMA kernel: bf16, head_dim D in {64, 128}, WAVES waves x 64 query rows.
+// MFMA kernel: bf16, head_dim D in {64, 128}, WAVES waves x 32 query rows.
 // --------------------------------------------------------------------------
+
+// Bits [j0, j0+32) of the 192-bit string {w1 : w0 : 64 ones}, read from bit
+// j0 + 64: pack-relative key positions j < 0 are prefix keys (all visible),
+// j in [0, 128) are the row's ancestor bits.  Requires -64 <= j0 < 128.
+__device__ __forceinline__ uint32_t vis_window(uint64_t w0, uint64_t w1, int j0) {
+    const int p = j0 + 64;
+    const int q = p >> 6, r = p & 63;
+    const uint64_t lo = q == 0 ? ~0ull : (q == 1 ? w0 : w1);
+    const uint64_t hi = q == 0 ? w0 : (q == 1 ? w1 : 0ull);
+    const uint64_t v = (lo >> r) | (r ? hi << (64 - r) : 0ull);
+    return (uint32_t)v;
+}
+
 template <int D, int WAVES>
-__global__ __launch_bounds__(WAVES * 64, 1) void tree_attn_mfma_kernel(AttnArgs a) {
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void tree_attn_mfma_kernel(AttnArgs a) {
     constexpr int NT = WAVES * 64;
-    constexpr int BN = 32;                 // keys per tile (one 32-row MFMA block)
+    constexpr int BN = 64;                 // keys per tile: two 32-key MFMA blocks
+    constexpr int ROWS = WAVES * 32;       // query rows per workgroup
     constexpr int KPAD = D + 8;            // K row stride in LDS (elements)
-    constexpr int VPAD = BN + 4;           // V^T row stride in LDS (elements)
+    constexpr int VPAD = BN + 8;           // V^T row stride in LDS (elements)
     constexpr int DSTEPS = D / 16;         // MFMA k-steps over the head dim
     constexpr int DB = D / 32;             // 32-row blocks of O^T
     constexpr int KCH = BN * D / 8;        // 16-byte K chunks per tile
     constexpr int K_PER_T = (KCH + NT - 1) / NT;
-    constexpr int VUNITS = (BN / 4) * (D / 8);   // (4 keys x 8 d) V units per tile
+    constexpr int OCT = BN / 8;            // 8-key groups per tile
+    constexpr int VUNITS = OCT * (D / 8);  // (8 keys x 8 d) V blocks per tile
     constexpr int V_PER_T = (VUNITS + NT - 1) / NT;
-    // With four waves the next tile is prefetched into registers during the
-    // MFMA work; narrower workgroups (small packs) load synchronously and rely
-    // on other resident workgroups to hide the latency.
-    constexpr bool PREFETCH = WAVES == 4;
+    // Four or more waves prefetch the next tile into registers during the MFMA
+    // work; narrower workgroups (small packs) load synchronously and rely on
+    // other resident workgroups to hide the latency.
+    constexpr bool PREFETCH = WAVES >= 4;
 
+    // K tile [key][d].  V tile transposed, [d][key'], with the keys of every
+    // 16-key group stored in the order (0-3, 8-11, 4-7, 12-15): a lane's eight
+    // P^T k-slots are then eight consecutive columns (one 16-byte read).
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VPAD];
 
@@ -163,112 +182,92 @@ __global__ __launch_bounds__(WAVES * 64, 1) void tree_attn_mfma_kernel(AttnArgs 
     const int g = lane >> 5;
     const int l32 = lane & 31;
     const int rows = sq.P * a.G;
-    const int row_base = rb * (WAVES * 64) + wave * 64;
-    const bool active = row_base < rows;
+    const int r = rb * ROWS + wave * 32 + l32;     // this lane's query row
+    const bool active = rb * ROWS + wave * 32 < rows;
+    const bool qvalid = r < rows;
+    const int qtok = sq.q0 + (qvalid ? r / a.G : 0);
+    const int qhead = h * a.G + (qvalid ? r % a.G : 0);
 
     const uint16_t *qp = static_cast<const uint16_t *>(a.q);
     const uint16_t *kp = static_cast<const uint16_t *>(a.k);
     const uint16_t *vp = static_cast<const uint16_t *>(a.v);
 
-    // ---- Q^T operands (B side): lane holds query l32 of each 32-row block,
-    // head-dim slice [ds*16 + g*8, +8)
-    bf16x8 qreg[2][DSTEPS];
-    uint64_t mw0[2], mw1[2];
-    int qtok[2], qhead[2];
-    bool qvalid[2];
+    // ---- Q^T operand (B side): query l32, head-dim slice [ds*16 + g*8, +8)
+    bf16x8 qreg[DSTEPS];
+    {
+        const uint16_t *src = qp + (int64_t)qtok * a.q_tok + (int64_t)qhead * a.q_head + g * 8;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        const int r = row_base + qb * 32 + l32;
-        qvalid[qb] = r < rows;
-        const int i = qvalid[qb] ? r / a.G : 0;
-        qtok[qb] = sq.q0 + i;
-        qhead[qb] = h * a.G + (qvalid[qb] ? r % a.G : 0);
-        const uint16_t *src = qp + (int64_t)qtok[qb] * a.q_tok + (int64_t)qhead[qb] * a.q_head + g * 8;
-#pragma unroll
-        for (int ds = 0; ds < DSTEPS; ++ds) {
-            if (qvalid[qb])
-                qreg[qb][ds] = *reinterpret_cast<const bf16x8 *>(src + ds * 16);
-            else
-                qreg[qb][ds] = bf16x8{};
-        }
-        mw0[qb] = 0;
-        mw1[qb] = 0;
-        if (qvalid[qb] && k_end > sq.S) {
-            const uint64_t *mp = a.mask + (int64_t)qtok[qb] * a.mask_words;
-            mw0[qb] = mp[0];
-            if (a.mask_words > 1) mw1[qb] = mp[1];
-        }
+        for (int ds = 0; ds < DSTEPS; ++ds)
+            qreg[ds] = qvalid ? *reinterpret_cast<const bf16x8 *>(src + ds * 16) : bf16x8{};
+    }
+    uint64_t mw0 = 0, mw1 = 0;
+    if (qvalid && k_end > sq.S) {
+        const uint64_t *mp = a.mask + (int64_t)qtok * a.mask_words;
+        mw0 = mp[0];
+        if (a.mask_words > 1) mw1 = mp[1];
     }
 
-    floatx16 o[2][DB];
+    floatx16 o[DB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[qb][db] = floatx16{};
-    float m[2] = {-INFINITY, -INFINITY};
-    float lsum[2] = {0.f, 0.f};
+    for (int db = 0; db < DB; ++db) o[db] = floatx16{};
+    float m = -INFINITY, msafe = 0.f, lsum = 0.f;
+    const float c = a.scale_log2;
 
     const int64_t kbase = (int64_t)sq.kv0 * a.k_tok + (int64_t)h * a.k_head;
     const int64_t vbase = (int64_t)sq.kv0 * a.v_tok + (int64_t)h * a.v_head;
 
     // ---- global -> register staging of one tile
     u32x4 kst[K_PER_T];
-    u32x4 vst[V_PER_T][4];
+    u32x4 vst[V_PER_T][8];
     auto fetch = [&](int t0) {
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
-            const int c = tid + it * NT;
-            if (c >= KCH) break;
-            const int key = c / (D / 8), dch = c % (D / 8);
+            const int cidx = tid + it * NT;
+            if (cidx >= KCH) break;
+            const int key = cidx / (D / 8), dch = cidx % (D / 8);
             const int kk = t0 + key;
-            if (kk < k_end)
-                kst[it] = *reinterpret_cast<const u32x4 *>(kp + kbase + (int64_t)kk * a.k_tok + dch * 8);
-            else
-                kst[it] = u32x4{0, 0, 0, 0};
+            kst[it] = kk < k_end ? *reinterpret_cast<const u32x4 *>(kp + kbase + (int64_t)kk * a.k_tok + dch * 8)
+                                 : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int it = 0; it < V_PER_T; ++it) {
             const int u = tid + it * NT;
             if (u >= VUNITS) break;
-            const int dch = u % (D / 8), kq = u / (D / 8);
+            const int oc = u % OCT, dch = u / OCT;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int kk = t0 + kq * 4 + j;
-                if (kk < k_end)
-                    vst[it][j] = *reinterpret_cast<const u32x4 *>(vp + vbase + (int64_t)kk * a.v_tok + dch * 8);
-                else
-                    vst[it][j] = u32x4{0, 0, 0, 0};
+            for (int i = 0; i < 8; ++i) {
+                // key i of stored group oc: 16*(oc/2) + 8*(i/4) + 4*(oc%2) + i%4
+                const int kk = t0 + 16 * (oc >> 1) + 8 * (i >> 2) + 4 * (oc & 1) + (i & 3);
+                vst[it][i] = kk < k_end
+                                 ? *reinterpret_cast<const u32x4 *>(vp + vbase + (int64_t)kk * a.v_tok + dch * 8)
+                                 : u32x4{0, 0, 0, 0};
             }
         }
     };
-    // ---- register -> LDS (K as is, V transposed to [d][key])
+    // ---- register -> LDS: K as is; V as 8x8 transposed blocks
     auto publish = [&](int buf) {
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
-            const int c = tid + it * NT;
-            if (c >= KCH) break;
-            const int key = c / (D / 8), dch = c % (D / 8);
+            const int cidx = tid + it * NT;
+            if (cidx >= KCH) break;
+            const int key = cidx / (D / 8), dch = cidx % (D / 8);
             *reinterpret_cast<u32x4 *>(&Ks[buf][key * KPAD + dch * 8]) = kst[it];
         }
 #pragma unroll
         for (int it = 0; it < V_PER_T; ++it) {
             const int u = tid + it * NT;
             if (u >= VUNITS) break;
-            const int dch = u % (D / 8), kq = u / (D / 8);
-            // vst[it][j] holds d = dch*8 .. +7 of key kq*4+j as 4 dwords of bf16
-            // pairs; row d of the transpose is (key0, key1, key2, key3) at d.
+            const int oc = u % OCT, dch = u / OCT;
 #pragma unroll
-            for (int dw = 0; dw < 4; ++dw) {
-                const uint32_t a0 = vst[it][0][dw], a1 = vst[it][1][dw];
-                const uint32_t a2 = vst[it][2][dw], a3 = vst[it][3][dw];
-                // low halves: d = dch*8 + 2*dw, high halves: d + 1
-                const u32x2 lo = {__builtin_amdgcn_perm(a1, a0, 0x05040100u),
-                                  __builtin_amdgcn_perm(a3, a2, 0x05040100u)};
-                const u32x2 hi = {__builtin_amdgcn_perm(a1, a0, 0x07060302u),
-                                  __builtin_amdgcn_perm(a3, a2, 0x07060302u)};
-                const int d = dch * 8 + 2 * dw;
-                *reinterpret_cast<u32x2 *>(&Vt[buf][d * VPAD + kq * 4]) = lo;
-                *reinterpret_cast<u32x2 *>(&Vt[buf][(d + 1) * VPAD + kq * 4]) = hi;
+            for (int dd = 0; dd < 8; ++dd) {
+                // dword dd/2 of each key holds d = 2*(dd/2) (low) and +1 (high)
+                const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
+                const int k = dd >> 1;
+                const u32x4 row = {__builtin_amdgcn_perm(vst[it][1][k], vst[it][0][k], sel),
+                                   __builtin_amdgcn_perm(vst[it][3][k], vst[it][2][k], sel),
+                                   __builtin_amdgcn_perm(vst[it][5][k], vst[it][4][k], sel),
+                                   __builtin_amdgcn_perm(vst[it][7][k], vst[it][6][k], sel)};
+                *reinterpret_cast<u32x4 *>(&Vt[buf][(dch * 8 + dd) * VPAD + oc * 8]) = row;
             }
         }
     };
@@ -284,135 +283,130 @@ __global__ __launch_bounds__(WAVES * 64, 1) void tree_attn_mfma_kernel(AttnArgs 
         if (PREFETCH && t + 1 < ntiles) fetch(t0 + BN);
         if (!active) continue;
 
-        // ---- S^T = K Q^T : 32 keys x (2 blocks of 32 queries)
-        floatx16 s[2] = {floatx16{}, floatx16{}};
+        // ---- S^T = K Q^T: two 32-key blocks x 32 queries
+        floatx16 s[2];
 #pragma unroll
-        for (int ds = 0; ds < DSTEPS; ++ds) {
-            const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(&Ks[buf][l32 * KPAD + ds * 16 + g * 8]);
+        for (int kb = 0; kb < 2; ++kb) {
+            s[kb] = floatx16{};
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
-                s[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[qb][ds], s[qb], 0, 0, 0);
+            for (int ds = 0; ds < DSTEPS; ++ds) {
+                const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(
+                    &Ks[buf][(kb * 32 + l32) * KPAD + ds * 16 + g * 8]);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[ds], s[kb], 0, 0, 0);
+            }
         }
 
-        // ---- visibility: tail of the split and the pack's ancestor words.
-        // Accumulator element r of lane (l32, g) is key 8*(r/4) + 4*g + r%4.
+        // ---- visibility (only tiles reaching the pack or the split's end).
+        // Element e of lane (l32, g) in block kb is key t0 + 32*kb + 4*g + off(e),
+        // off(e) = 8*(e/4) + e%4.
         if (t0 + BN > sq.S || t0 + BN > k_end) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = t0 + 8 * (r >> 2) + 4 * g + (r & 3);
+            for (int kb = 0; kb < 2; ++kb) {
+                const int k0 = t0 + kb * 32 + 4 * g;
+                const int lim = k_end - k0;
+                uint32_t vis = vis_window(mw0, mw1, k0 - sq.S);
+                vis &= lim >= 32 ? ~0u : (lim <= 0 ? 0u : ((1u << lim) - 1u));
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) {
-                    const bool vis = key < k_end && (key < sq.S || pack_bit(key - sq.S, mw0[qb], mw1[qb]));
-                    if (!vis) s[qb][r] = -INFINITY;
+                for (int e = 0; e < 16; ++e) {
+                    const int off = 8 * (e >> 2) + (e & 3);
+                    s[kb][e] = (vis >> off) & 1u ? s[kb][e] : -INFINITY;
                 }
             }
         }
 
-        // ---- online softmax (base 2, lazy rescale)
-        bool need_any = false;
-        float mt[2];
+        // ---- online softmax in base 2.  The running max m is shared by the
+        // two lanes (l32, 0) and (l32, 1) of a query; it only moves when a
+        // tile exceeds it by more than 2^kRescaleSlack somewhere in the wave,
+        // so the cross-lane exchange and the O rescale are rare.
+        float lmax = s[0][0];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            float mx = s[qb][0];
+        for (int e = 1; e < 16; ++e) lmax = fmaxf(lmax, s[0][e]);
 #pragma unroll
-            for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[qb][r]);
-            mx = fmaxf(mx, partner32(mx));
-            mt[qb] = mx * a.scale_log2;
-            need_any |= mt[qb] > m[qb] + kRescaleSlack;
+        for (int e = 0; e < 16; ++e) lmax = fmaxf(lmax, s[1][e]);
+        if (__any(lmax * c > m + kRescaleSlack)) {
+            const float mx = fmaxf(lmax, partner32(lmax)) * c;
+            const float mn = fmaxf(m, mx);
+            const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[db] *= alpha;
+            m = mn;
+            msafe = m == -INFINITY ? 0.f : m;
         }
-        if (__any(need_any)) {
+        bf16x8 pb[2][2];   // [kb][half]: P^T operand, 8 k-slots each
+        float acc = 0.f;
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                const float mn = fmaxf(m[qb], mt[qb]);
-                const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[qb] - mn);
-                lsum[qb] *= alpha;
-#pragma unroll
-                for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
-                m[qb] = mn;
-            }
-        }
-        bf16x8 pb[2][2];   // [qb][half]: P^T operand, k-slots of 16 keys
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const float msafe = m[qb] == -INFINITY ? 0.f : m[qb];
-            float acc = 0.f;
+        for (int kb = 0; kb < 2; ++kb) {
             float p[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                p[r] = __builtin_amdgcn_exp2f(fmaf(s[qb][r], a.scale_log2, -msafe));
-                acc += p[r];
+            for (int e = 0; e < 16; ++e) {
+                p[e] = __builtin_amdgcn_exp2f(fmaf(s[kb][e], c, -msafe));
+                acc += p[e];
             }
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
+            for (int hf = 0; hf < 2; ++hf) {
                 u32x4 w;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[half * 8 + 2 * e], p[half * 8 + 2 * e + 1]);
-                pb[qb][half] = __builtin_bit_cast(bf16x8, w);
+                for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[hf * 8 + 2 * e], p[hf * 8 + 2 * e + 1]);
+                pb[kb][hf] = __builtin_bit_cast(bf16x8, w);
             }
-            lsum[qb] += acc;
         }
+        lsum += acc;
 
-        // ---- O^T += V^T P^T over 2 slices of 16 keys.  Slot j of lane group
-        // g is key 16*half + 8*(j/4) + 4*g + j%4 on both operands.
+        // ---- O^T += V^T P^T over four 16-key slices.  Slot j of lane group g
+        // in slice (kb, hf) is key 32*kb + 16*hf + 8*(j/4) + 4*g + j%4, stored
+        // at column 32*kb + 16*hf + 8*g + j.
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const uint16_t *vrow = &Vt[buf][(db * 32 + l32) * VPAD + half * 16 + 4 * g];
-                const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow);
-                const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + 8);
-                const u32x4 va4 = {lo[0], lo[1], hi[0], hi[1]};
-                const bf16x8 va = __builtin_bit_cast(bf16x8, va4);
+            for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb)
-                    o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[qb][half], o[qb][db], 0, 0, 0);
-            }
-        }
+                for (int db = 0; db < DB; ++db) {
+                    const bf16x8 va = *reinterpret_cast<const bf16x8 *>(
+                        &Vt[buf][(db * 32 + l32) * VPAD + kb * 32 + hf * 16 + g * 8]);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb][hf], o[db], 0, 0, 0);
+                }
     }
 
     if (!active) return;
     // ---- epilogue: normalise, write the output or the split partial.
-    // O^T element r of lane (l32, g) in block db is d = 32*db + 8*(r/4) + 4*g + r%4.
+    // O^T element e of lane (l32, g) in block db is d = 32*db + 8*(e/4) + 4*g + e%4.
+    const float ltot = lsum + partner32(lsum);
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
+    if (!qvalid) return;
+    if (sq.ns == 1) {
+        uint16_t *op = static_cast<uint16_t *>(a.out) + (int64_t)qtok * a.o_tok + (int64_t)qhead * a.o_head;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-        const float ltot = lsum[qb] + partner32(lsum[qb]);
-        const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-        const float lse2 = ltot > 0.f ? (m[qb] == -INFINITY ? 0.f : m[qb]) + log2f(ltot) : -INFINITY;
-        if (!qvalid[qb]) continue;
-        if (sq.ns == 1) {
-            uint16_t *op = static_cast<uint16_t *>(a.out) + (int64_t)qtok[qb] * a.o_tok + (int64_t)qhead[qb] * a.o_head;
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
-                    const int d = db * 32 + 8 * r4 + 4 * g;
-                    const u32x2 w = {pack_bf16x2(o[qb][db][4 * r4] * inv, o[qb][db][4 * r4 + 1] * inv),
-                                     pack_bf16x2(o[qb][db][4 * r4 + 2] * inv, o[qb][db][4 * r4 + 3] * inv)};
-                    *reinterpret_cast<u32x2 *>(op + d) = w;
-                }
-            if (a.lse && g == 0) a.lse[(int64_t)qtok[qb] * a.Hq + qhead[qb]] = lse2 * kLn2;
-        } else {
-            const int i = qtok[qb] - sq.q0;
-            const int64_t prow = sq.part_off + (int64_t)split * sq.P + i;
-            if (prow >= a.part_rows) {
-                raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
-                continue;
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = db * 32 + 8 * r4 + 4 * g;
+                const u32x2 w = {pack_bf16x2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv),
+                                 pack_bf16x2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv)};
+                *reinterpret_cast<u32x2 *>(op + d) = w;
             }
-            float *pp = a.part_o + (prow * a.Hq + qhead[qb]) * D;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
-                    const int d = db * 32 + 8 * r4 + 4 * g;
-                    const floatx4 w = {o[qb][db][4 * r4] * inv, o[qb][db][4 * r4 + 1] * inv,
-                                       o[qb][db][4 * r4 + 2] * inv, o[qb][db][4 * r4 + 3] * inv};
-                    *reinterpret_cast<floatx4 *>(pp + d) = w;
-                }
-            if (g == 0) a.part_lse[prow * a.Hq + qhead[qb]] = lse2;
+        if (a.lse && g == 0) a.lse[(int64_t)qtok * a.Hq + qhead] = lse2 * kLn2;
+    } else {
+        const int i = qtok - sq.q0;
+        const int64_t prow = sq.part_off + (int64_t)split * sq.P + i;
+        if (prow >= a.part_rows) {
+            raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+            return;
         }
+        float *pp = a.part_o + (prow * a.Hq + qhead) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int d = db * 32 + 8 * r4 + 4 * g;
+                const floatx4 w = {o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
+                                   o[db][4 * r4 + 3] * inv};
+                *reinterpret_cast<floatx4 *>(pp + d) = w;
+            }
+        if (g == 0) a.part_lse[prow * a.Hq + qhead] = lse2;
     }
 }
-
 // --------------------------------------------------------------------------
 // Split-K combine: one workgroup per packed token, all query heads.
 // --------------------------------------------------------------------------
@@ -573,10 +567,11 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
 // --------------------------------------------------------------------------
 static bool mfma_path(int32_t dtype, int32_t D) { return dtype == CAST_BF16 && (D == 64 || D == 128); }
 
+// Waves per workgroup (32 query rows each) for the largest possible pack.
 static int waves_for(int32_t total_q, int32_t G) {
     const int pmax = total_q < kMaxPack ? total_q : kMaxPack;
     const int rows = pmax * G;
-    return rows <= 64 ? 1 : rows <= 128 ? 2 : 4;
+    return rows <= 64 ? 2 : rows <= 128 ? 4 : 8;
 }
 
 static int32_t resolve_chunk(int32_t batch, int32_t total_q, int32_t total_kv, int32_t Hq, int32_t Hkv,
@@ -584,7 +579,7 @@ static int32_t resolve_chunk(int32_t batch, int32_t total_q, int32_t total_kv, i
     if (!mfma_path(dtype, D) || kv_split < 0 || batch <= 0) return kNoSplit;
     if (kv_split > 0) return ((kv_split + 63) / 64) * 64;
     const int G = Hq / Hkv;
-    const int rows_wg = waves_for(total_q, G) * 64;
+    const int rows_wg = waves_for(total_q, G) * 32;
     const int64_t p_avg = (total_q + batch - 1) / batch;
     const int64_t p_est = p_avg < kMaxPack ? p_avg : kMaxPack;
     const int64_t rb = (p_est * G + rows_wg - 1) / rows_wg;
@@ -700,7 +695,7 @@ static int tree_attn_run(const void *q, const void *k, const void *v, void *out,
     }
 
     const int waves = waves_for(total_q, a.G);
-    a.rows_wg = waves * 64;
+    a.rows_wg = waves * 32;
     a.chunk = resolve_chunk(batch, total_q, total_kv, num_q_heads, num_kv_heads, head_dim, dtype, kv_split);
     if (a.chunk != kNoSplit) {
         const size_t need = cast_tree_attn_workspace_size(batch, total_q, total_kv, num_q_heads, num_kv_heads,
@@ -724,13 +719,13 @@ static int tree_attn_run(const void *q, const void *k, const void *v, void *out,
 #define CAST_LAUNCH(DD, W) tree_attn_mfma_kernel<DD, W><<<grid, W * 64, 0, st>>>(a)
     if (!(stages & kStageAttn)) {
     } else if (head_dim == 128) {
-        if (waves == 1) CAST_LAUNCH(128, 1);
-        else if (waves == 2) CAST_LAUNCH(128, 2);
-        else CAST_LAUNCH(128, 4);
+        if (waves == 2) CAST_LAUNCH(128, 2);
+        else if (waves == 4) CAST_LAUNCH(128, 4);
+        else CAST_LAUNCH(128, 8);
     } else {
-        if (waves == 1) CAST_LAUNCH(64, 1);
-        else if (waves == 2) CAST_LAUNCH(64, 2);
-        else CAST_LAUNCH(64, 4);
+        if (waves == 2) CAST_LAUNCH(64, 2);
+        else if (waves == 4) CAST_LAUNCH(64, 4);
+        else CAST_LAUNCH(64, 8);
     }
 #undef CAST_LAUNCH
     if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
