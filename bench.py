@@ -186,6 +186,8 @@ def main():
     ap.add_argument("--kv-split", type=int, default=0, help="keys per split-K chunk (0: library choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 launches), to scale HBM byte counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -197,6 +199,17 @@ def main():
     import torch
     from cast_amd import scenarios
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        # an elementwise kernel (negation), not copy_(): a same-dtype copy_
+        # may go to a DMA engine that the shader counters do not see
+        n = args.copy_calibration << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
+        return
     log(f"device: {torch.cuda.get_device_name(dev)}")
     wl = scenarios.qwen3_headline()
     h = Harness(wl, dev, sets=args.sets, kv_split=args.kv_split)
@@ -205,7 +218,9 @@ def main():
     t = h.time(args.steps, args.warmup)
     log(f"  call {t['call_us']:.1f} us (mean {t['call_mean_us']:.1f}), attention kernel {t['attn_us']:.1f} us, "
         f"combine {t['combine_us']:.1f} us, host wall {t['wall_us']:.1f} us/call")
-    rl = roofline(wl, t["attn_us"] * 1e-6)
+    # achieved = algorithmic work per launch / mean launch duration (HIP events
+    # on the launch stream), comparable with the profiler's average duration
+    rl = roofline(wl, t["attn_mean_us"] * 1e-6)
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
