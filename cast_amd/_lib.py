@@ -19,6 +19,7 @@ ERR_HIP = 10
 FLAG_BAD_PACK = 1
 FLAG_BAD_OFFSETS = 2
 FLAG_BAD_PARENT = 4
+FLAG_TOO_LONG = 8
 
 BF16, FP32 = 0, 1
 
@@ -37,6 +38,8 @@ SIGNATURES = {
     "cast_tree_attn_fwd": (_ATTN_ARGS, ctypes.c_int),
     "cast_tree_attn_partial": (_ATTN_ARGS, ctypes.c_int),
     "cast_tree_attn_combine": (_ATTN_ARGS, ctypes.c_int),
+    "cast_tree_attn_store_fwd": ([_P] * 11 + [_I32] * 8 + [_I64] * 14 + [_I32, ctypes.c_float, _I32, _P, _SZ, _P, _P],
+                                 ctypes.c_int),
     "cast_tree_attn_workspace_size": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32], _SZ),
     "cast_tree_attn_default_split": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32], _I32),
     "cast_greedy_accept": ([_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P], ctypes.c_int),
@@ -106,4 +109,6 @@ def raise_device_flags(flags, what):
         parts.append("cu_q / cu_kv / prefix_len / pack_len are inconsistent")
     if flags & FLAG_BAD_PARENT:
         parts.append("a parent index is not in [-1, own index)")
+    if flags & FLAG_TOO_LONG:
+        parts.append("a request's keys exceed the kernel's row addressing (2^24 rows / 2 GiB per source)")
     raise ValueError(f"{what}: " + "; ".join(parts))

@@ -22,7 +22,10 @@
 // moves only when a tile raises it by more than 2^8, so most tiles skip the
 // O rescale.  Long prefixes are split over keys; a combine kernel merges the
 // per-split (O, lse) pairs by log-sum-exp.
+#include <limits.h>
 #include <math.h>
+
+#include <type_traits>
 
 #include "cast_common.hpp"
 
@@ -34,17 +37,35 @@ constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kRescaleSlack = 8.0f;    // log2 headroom before the O rescale
 
+// Where the keys and values of request b, KV head h live.  Two layouts:
+//  concat (store == 0): one ragged [total_kv, Hkv, D] tensor per K and V;
+//      request b owns rows [cu_kv[b], cu_kv[b+1]) = concat(prefix, pack)
+//      (cast_trees/tree_attn.py:71).  pre == pack, pre_b unused.
+//  store (store == 1): the prefix stays in a per-request store
+//      [B, Hkv, cap, D] (cast_trees/serving.py:191-205), key t of request b
+//      at pre + b*pre_b + h*pre_h + t*pre_t; the pack comes from the
+//      forward's own K/V [Hkv, total_q, D], key j at
+//      pack + h*pack_h + (cu_q[b] + j)*pack_t.
+struct KvSource {
+    const void *k_pre, *v_pre, *k_pack, *v_pack;
+    int64_t kpre_b, kpre_h, kpre_t, vpre_b, vpre_h, vpre_t;
+    int64_t kpack_h, kpack_t, vpack_h, vpack_t;
+    int32_t store, cap;
+};
+
 struct AttnArgs {
-    const void *q, *k, *v;
+    const void *q;
+    KvSource kv;
     void *out;
     float *lse;
     const int32_t *cu_q, *cu_kv, *prefix_len, *pack_len;
     const uint64_t *mask;
     int32_t mask_words;
     int32_t batch, total_q, total_kv, Hq, Hkv, G;
-    int64_t q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head;
+    int64_t q_tok, q_head, o_tok, o_head;
     float scale_log2;   // sm_scale * log2(e)
     int32_t chunk;      // keys per split, multiple of 64 (kNoSplit = no split)
+    int32_t max_rows;   // longest key source (rows) the MFMA kernel can address
     int32_t rows_wg;    // query rows per workgroup
     float *part_o;      // [part_rows][Hq][D] fp32, normalised partial outputs
     float *part_lse;    // [part_rows][Hq]    fp32, base-2 partial lse
@@ -61,9 +82,20 @@ struct Seq {
 __device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s) {
     const int S = a.prefix_len[b], P = a.pack_len[b];
     const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
-    const int kv0 = a.cu_kv[b], kv1 = a.cu_kv[b + 1];
-    if (S < 0 || q0 < 0 || kv0 < 0 || q1 > a.total_q || kv1 > a.total_kv || q1 - q0 != P ||
-        kv1 - kv0 != S + P) {
+    int kv0 = 0, kv1 = S + P;
+    bool bad_kv;
+    if (a.kv.store) {
+        bad_kv = S > a.kv.cap;
+    } else {
+        kv0 = a.cu_kv[b];
+        kv1 = a.cu_kv[b + 1];
+        bad_kv = kv0 < 0 || kv1 > a.total_kv || kv1 - kv0 != S + P;
+    }
+    if ((a.kv.store ? max(S, P) : S + P) > a.max_rows) {
+        if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_TOO_LONG);
+        return false;
+    }
+    if (S < 0 || q0 < 0 || q1 > a.total_q || q1 - q0 != P || bad_kv) {
         if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         return false;
     }
@@ -86,10 +118,21 @@ __device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s) {
 
 // Total work items and, for item w, the request and in-request index.
 // Items are ordered (b, h, split, row block) with the row block fastest.
+// In the store layout total_kv is a caller-supplied bound on sum(S_b + P_b)
+// that sized the grid and the workspace; a batch exceeding it is rejected
+// whole.  (The concat layout checks every request against it in load_seq.)
+__device__ __forceinline__ bool store_total_ok(const AttnArgs &a, int64_t kv_sum) {
+    if (a.kv.store && kv_sum > a.total_kv) {
+        if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        return false;
+    }
+    return true;
+}
+
 __device__ bool find_item(const AttnArgs &a, int w, Seq &s, int &local, int &total) {
     total = 0;
     bool found = false;
-    int64_t part = 0;
+    int64_t part = 0, kv_sum = 0;
     for (int b = 0; b < a.batch; ++b) {
         Seq t;
         if (!load_seq(a, b, t)) continue;
@@ -101,10 +144,50 @@ __device__ bool find_item(const AttnArgs &a, int w, Seq &s, int &local, int &tot
             found = true;
         }
         total += n;
+        kv_sum += t.T;
         if (t.ns > 1) part += (int64_t)t.ns * t.P;
+    }
+    if (!store_total_ok(a, kv_sum)) {
+        total = 0;
+        return false;
     }
     return found;
 }
+
+// Base pointers and token strides of the prefix and pack keys of one
+// (request, KV head); key kk < S is prefix key kk, key kk >= S pack key kk - S.
+template <typename T>
+struct KvView {
+    const T *kpre, *kpack, *vpre, *vpack;
+    int64_t kpre_t, kpack_t, vpre_t, vpack_t;
+
+    __device__ __forceinline__ KvView(const KvSource &src, const Seq &s, int h) {
+        const T *kp = static_cast<const T *>(src.k_pre), *vp = static_cast<const T *>(src.v_pre);
+        kpre_t = src.kpre_t;
+        vpre_t = src.vpre_t;
+        if (src.store) {
+            kpre = kp + (int64_t)s.b * src.kpre_b + (int64_t)h * src.kpre_h;
+            vpre = vp + (int64_t)s.b * src.vpre_b + (int64_t)h * src.vpre_h;
+            kpack = static_cast<const T *>(src.k_pack) + (int64_t)s.q0 * src.kpack_t + (int64_t)h * src.kpack_h;
+            vpack = static_cast<const T *>(src.v_pack) + (int64_t)s.q0 * src.vpack_t + (int64_t)h * src.vpack_h;
+            kpack_t = src.kpack_t;
+            vpack_t = src.vpack_t;
+        } else {
+            kpre = kp + (int64_t)s.kv0 * kpre_t + (int64_t)h * src.kpre_h;
+            vpre = vp + (int64_t)s.kv0 * vpre_t + (int64_t)h * src.vpre_h;
+            kpack = kpre + (int64_t)s.S * kpre_t;
+            vpack = vpre + (int64_t)s.S * vpre_t;
+            kpack_t = kpre_t;
+            vpack_t = vpre_t;
+        }
+    }
+    __device__ __forceinline__ const T *key(int kk, int S) const {
+        return kk < S ? kpre + (int64_t)kk * kpre_t : kpack + (int64_t)(kk - S) * kpack_t;
+    }
+    __device__ __forceinline__ const T *val(int kk, int S) const {
+        return kk < S ? vpre + (int64_t)kk * vpre_t : vpack + (int64_t)(kk - S) * vpack_t;
+    }
+};
 
 __device__ __forceinline__ bool pack_bit(int j, uint64_t w0, uint64_t w1) {
     const uint64_t w = j < 64 ? w0 : w1;
@@ -127,7 +210,30 @@ __device__ __forceinline__ uint32_t vis_window(uint64_t w0, uint64_t w1, int j0)
     return (uint32_t)v;
 }
 
-template <int D, int WAVES>
+// What the MFMA kernel's epilogue needs, parked in LDS during the key loop
+// so that it holds no scalar registers there.
+struct EpiArgs {
+    void *out;
+    float *lse, *part_o, *part_lse;
+    int32_t *status;
+    int64_t o_tok, o_head, part_rows;
+    int64_t prow0;      // partial row of token q0 + i is prow0 + q0 + i
+    int32_t ns, Hq;
+};
+
+// Raw buffer resource over `rows` key rows of `row_bytes` stride and
+// `width` bytes each, from base: loads at offsets past the last row's end
+// return zeros.  The caller keeps rows * row_bytes below 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t seg_rsrc(const void *base, int rows, uint32_t row_bytes,
+                                                           uint32_t width) {
+    const uint32_t bytes = rows > 0 ? (uint32_t)(rows - 1) * row_bytes + width : 0u;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+template <int D, int WAVES, bool STORE>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void tree_attn_mfma_kernel(AttnArgs a) {
     constexpr int NT = WAVES * 64;
@@ -152,6 +258,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     // P^T k-slots are then eight consecutive columns (one 16-byte read).
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VPAD];
+    __shared__ EpiArgs epi;
 
     // ---- which unit is this workgroup?  Work items are renumbered so that
     // consecutive items (the row blocks of one key split) run on one XCD
@@ -189,8 +296,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     const int qhead = h * a.G + (qvalid ? r % a.G : 0);
 
     const uint16_t *qp = static_cast<const uint16_t *>(a.q);
-    const uint16_t *kp = static_cast<const uint16_t *>(a.k);
-    const uint16_t *vp = static_cast<const uint16_t *>(a.v);
+    const KvView<uint16_t> kv(a.kv, sq, h);
 
     // ---- Q^T operand (B side): query l32, head-dim slice [ds*16 + g*8, +8)
     bf16x8 qreg[DSTEPS];
@@ -213,35 +319,59 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     float m = -INFINITY, msafe = 0.f, lsum = 0.f;
     const float c = a.scale_log2;
 
-    const int64_t kbase = (int64_t)sq.kv0 * a.k_tok + (int64_t)h * a.k_head;
-    const int64_t vbase = (int64_t)sq.kv0 * a.v_tok + (int64_t)h * a.v_head;
+    // ---- key tiles, each covering keys [t0, t0 + valid), valid <= BN (the
+    // rest of the tile is masked).  The split's prefix keys [k_begin, pre_end)
+    // and pack keys [pk_begin, k_end) are tiled separately: in the store
+    // layout every tile then reads one source, and both layouts add up the
+    // same keys in the same order.
+    const int pre_end = min(k_end, sq.S);
+    const int n_pre = k_begin < pre_end ? (pre_end - k_begin + BN - 1) / BN : 0;
+    const int pk_begin = max(k_begin, sq.S);
+    const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
+    const int ntiles = n_pre + n_pack;
+    auto tile_t0 = [&](int t) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
+    auto tile_valid = [&](int t) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
 
-    // ---- global -> register staging of one tile
+    // ---- global -> register staging of one tile.  Each key source of this
+    // (request, head) is one buffer resource that ends at its last row (the
+    // concat layout: the request's S+P rows; the store layout: its S prefix
+    // slots and its P pack rows), so rows past it read as zeros; a tile adds
+    // 32-bit byte offsets (row * row stride + 16-byte chunk).  Rows past a
+    // split's end but inside the request are real keys, masked below.
+    const uint32_t ksb_pre = (uint32_t)kv.kpre_t * 2u, vsb_pre = (uint32_t)kv.vpre_t * 2u;
+    const uint32_t ksb_pack = (uint32_t)kv.kpack_t * 2u, vsb_pack = (uint32_t)kv.vpack_t * 2u;
+    const int rows_pre = STORE ? sq.S : sq.T;
+    const __amdgpu_buffer_rsrc_t kr_pre = seg_rsrc(kv.kpre, rows_pre, ksb_pre, D * 2);
+    const __amdgpu_buffer_rsrc_t vr_pre = seg_rsrc(kv.vpre, rows_pre, vsb_pre, D * 2);
+    const __amdgpu_buffer_rsrc_t kr_pack = seg_rsrc(kv.kpack, STORE ? sq.P : 0, ksb_pack, D * 2);
+    const __amdgpu_buffer_rsrc_t vr_pack = seg_rsrc(kv.vpack, STORE ? sq.P : 0, vsb_pack, D * 2);
     u32x4 kst[K_PER_T];
     u32x4 vst[V_PER_T][8];
-    auto fetch = [&](int t0) {
+    auto fetch = [&](int t) {
+        const bool pre = !STORE || t < n_pre;
+        const int t0 = tile_t0(t);
+        const uint32_t row0 = (uint32_t)(pre ? t0 : t0 - sq.S);   // first row within its source
+        const __amdgpu_buffer_rsrc_t krs = pre ? kr_pre : kr_pack;
+        const __amdgpu_buffer_rsrc_t vrs = pre ? vr_pre : vr_pack;
+        const uint32_t ksb = pre ? ksb_pre : ksb_pack;
+        const uint32_t vsb = pre ? vsb_pre : vsb_pack;
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
             const int cidx = tid + it * NT;
             if (cidx >= KCH) break;
             const int key = cidx / (D / 8), dch = cidx % (D / 8);
-            const int kk = t0 + key;
-            kst[it] = kk < k_end ? *reinterpret_cast<const u32x4 *>(kp + kbase + (int64_t)kk * a.k_tok + dch * 8)
-                                 : u32x4{0, 0, 0, 0};
+            kst[it] = load16(krs, __umul24(row0 + key, ksb) + dch * 16);
         }
 #pragma unroll
         for (int it = 0; it < V_PER_T; ++it) {
             const int u = tid + it * NT;
             if (u >= VUNITS) break;
             const int oc = u % OCT, dch = u / OCT;
+            // key i of stored group oc: 16*(oc/2) + 4*(oc%2) + 8*(i/4) + i%4
+            const uint32_t v0 = row0 + 16 * (oc >> 1) + 4 * (oc & 1);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                // key i of stored group oc: 16*(oc/2) + 8*(i/4) + 4*(oc%2) + i%4
-                const int kk = t0 + 16 * (oc >> 1) + 8 * (i >> 2) + 4 * (oc & 1) + (i & 3);
-                vst[it][i] = kk < k_end
-                                 ? *reinterpret_cast<const u32x4 *>(vp + vbase + (int64_t)kk * a.v_tok + dch * 8)
-                                 : u32x4{0, 0, 0, 0};
-            }
+            for (int i = 0; i < 8; ++i)
+                vst[it][i] = load16(vrs, __umul24(v0 + 8 * (i >> 2) + (i & 3), vsb) + dch * 16);
         }
     };
     // ---- register -> LDS: K as is; V as 8x8 transposed blocks
@@ -272,15 +402,29 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         }
     };
 
-    const int ntiles = (k_end - k_begin + BN - 1) / BN;
-    if (PREFETCH && ntiles > 0) fetch(k_begin);
+    if (tid == 0) {
+        epi.out = a.out;
+        epi.lse = a.lse;
+        epi.part_o = a.part_o;
+        epi.part_lse = a.part_lse;
+        epi.status = a.status;
+        epi.o_tok = a.o_tok;
+        epi.o_head = a.o_head;
+        epi.part_rows = a.part_rows;
+        epi.prow0 = sq.part_off + (int64_t)split * sq.P - sq.q0;
+        epi.ns = sq.ns;
+        epi.Hq = a.Hq;
+    }
+    __syncthreads();
+    if (PREFETCH && ntiles > 0) fetch(0);
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t & 1;
-        const int t0 = k_begin + t * BN;
-        if (!PREFETCH) fetch(t0);
+        const int t0 = tile_t0(t);
+        const int valid = tile_valid(t);
+        if (!PREFETCH) fetch(t);
         publish(buf);
         __syncthreads();
-        if (PREFETCH && t + 1 < ntiles) fetch(t0 + BN);
+        if (PREFETCH && t + 1 < ntiles) fetch(t + 1);
         if (!active) continue;
 
         // ---- S^T = K Q^T: two 32-key blocks x 32 queries
@@ -296,15 +440,16 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             }
         }
 
-        // ---- visibility (only tiles reaching the pack or the split's end).
-        // Element e of lane (l32, g) in block kb is key t0 + 32*kb + 4*g + off(e),
-        // off(e) = 8*(e/4) + e%4.
-        if (t0 + BN > sq.S || t0 + BN > k_end) {
+        // ---- visibility (pack tiles and partial tiles only).  Element e of
+        // lane (l32, g) in block kb is key t0 + 32*kb + 4*g + off(e),
+        // off(e) = 8*(e/4) + e%4; in a pack tile that is pack key t0 - S + ...
+        const bool pack_tile = t >= n_pre;
+        if (pack_tile || valid < BN) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const int k0 = t0 + kb * 32 + 4 * g;
-                const int lim = k_end - k0;
-                uint32_t vis = vis_window(mw0, mw1, k0 - sq.S);
+                const int k0 = kb * 32 + 4 * g;
+                const int lim = valid - k0;
+                uint32_t vis = pack_tile ? vis_window(mw0, mw1, t0 - sq.S + k0) : ~0u;
                 vis &= lim >= 32 ? ~0u : (lim <= 0 ? 0u : ((1u << lim) - 1u));
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
@@ -375,8 +520,9 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
     const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
     if (!qvalid) return;
-    if (sq.ns == 1) {
-        uint16_t *op = static_cast<uint16_t *>(a.out) + (int64_t)qtok * a.o_tok + (int64_t)qhead * a.o_head;
+    const EpiArgs e = epi;
+    if (e.ns == 1) {
+        uint16_t *op = static_cast<uint16_t *>(e.out) + (int64_t)qtok * e.o_tok + (int64_t)qhead * e.o_head;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -386,15 +532,14 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                                  pack_bf16x2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv)};
                 *reinterpret_cast<u32x2 *>(op + d) = w;
             }
-        if (a.lse && g == 0) a.lse[(int64_t)qtok * a.Hq + qhead] = lse2 * kLn2;
+        if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
     } else {
-        const int i = qtok - sq.q0;
-        const int64_t prow = sq.part_off + (int64_t)split * sq.P + i;
-        if (prow >= a.part_rows) {
-            raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        const int64_t prow = e.prow0 + qtok;
+        if (prow >= e.part_rows) {
+            raise_flag(e.status, CAST_FLAG_BAD_OFFSETS);
             return;
         }
-        float *pp = a.part_o + (prow * a.Hq + qhead) * D;
+        float *pp = e.part_o + (prow * e.Hq + qhead) * D;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -404,7 +549,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                                    o[db][4 * r4 + 3] * inv};
                 *reinterpret_cast<floatx4 *>(pp + d) = w;
             }
-        if (g == 0) a.part_lse[prow * a.Hq + qhead] = lse2;
+        if (g == 0) e.part_lse[prow * e.Hq + qhead] = lse2;
     }
 }
 // --------------------------------------------------------------------------
@@ -415,18 +560,21 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     const int tok = blockIdx.x;
     Seq sq;
     bool found = false;
-    int64_t part = 0;
-    for (int b = 0; b < a.batch && !found; ++b) {
+    int64_t part = 0, kv_sum = 0;
+    // the store layout checks the whole batch against its total_kv bound;
+    // the concat layout can stop at its own request
+    for (int b = 0; b < a.batch && !(found && !a.kv.store); ++b) {
         Seq t;
         if (!load_seq(a, b, t)) continue;
-        if (tok >= t.q0 && tok < t.q0 + t.P) {
+        if (!found && tok >= t.q0 && tok < t.q0 + t.P) {
             sq = t;
             sq.part_off = part;
             found = true;
         }
+        kv_sum += t.T;
         if (t.ns > 1) part += (int64_t)t.ns * t.P;
     }
-    if (!found || sq.ns <= 1) return;
+    if (!store_total_ok(a, kv_sum) || !found || sq.ns <= 1) return;
     const int i = tok - sq.q0;
     if (sq.part_off + (int64_t)sq.ns * sq.P > a.part_rows) return;
     constexpr int C = D / 4;
@@ -491,8 +639,7 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
     const int tok = sq.q0 + (valid ? r / a.G : 0);
     const int hq = h * a.G + (valid ? r % a.G : 0);
     const T *qp = static_cast<const T *>(a.q);
-    const T *kp = static_cast<const T *>(a.k);
-    const T *vp = static_cast<const T *>(a.v);
+    const KvView<T> kv(a.kv, sq, h);
     for (int d = sub; d < D; d += 16)
         Qs[row][d] = valid ? load_elem(qp + (int64_t)tok * a.q_tok + (int64_t)hq * a.q_head + d) : 0.f;
     uint64_t w0 = 0, w1 = 0;
@@ -511,8 +658,8 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
             const int key = c / D, d = c % D;
             const int kk = t0 + key;
             const bool in = kk < sq.T;
-            Ks[key][d] = in ? load_elem(kp + (int64_t)(sq.kv0 + kk) * a.k_tok + (int64_t)h * a.k_head + d) : 0.f;
-            Vs[key][d] = in ? load_elem(vp + (int64_t)(sq.kv0 + kk) * a.v_tok + (int64_t)h * a.v_head + d) : 0.f;
+            Ks[key][d] = in ? load_elem(kv.key(kk, sq.S) + d) : 0.f;
+            Vs[key][d] = in ? load_elem(kv.val(kk, sq.S) + d) : 0.f;
         }
         __syncthreads();
         float sv[2];
@@ -626,37 +773,51 @@ extern "C" size_t cast_tree_attn_workspace_size(int32_t batch, int32_t total_q, 
 
 enum { kStageAttn = 1, kStageCombine = 2 };
 
-static int tree_attn_run(const void *q, const void *k, const void *v, void *out, float *lse, const int32_t *cu_q,
+static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *lse, const int32_t *cu_q,
                          const int32_t *cu_kv, const int32_t *prefix_len, const int32_t *pack_len,
                          const uint64_t *mask, int32_t mask_words, int32_t batch, int32_t total_q, int32_t total_kv,
                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
-                         int64_t k_tok, int64_t k_head, int64_t v_tok, int64_t v_head, int64_t o_tok,
-                         int64_t o_head, int32_t dtype, float sm_scale, int32_t kv_split, void *workspace,
-                         size_t workspace_bytes, int32_t *status, cast_stream_t stream, int stages) {
+                         int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale, int32_t kv_split,
+                         void *workspace, size_t workspace_bytes, int32_t *status, cast_stream_t stream, int stages) {
     if (batch < 0 || total_q < 0 || total_kv < 0 || head_dim <= 0) return CAST_ERR_SHAPE;
     if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return CAST_ERR_HEAD_RATIO;
     if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
     if (mask_words != 1 && mask_words != 2) return CAST_ERR_SHAPE;
+    if (kv.store && kv.cap < 0) return CAST_ERR_SHAPE;
     if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return CAST_ERR_SCALE;
     if (batch == 0 || total_q == 0) return CAST_OK;
-    if (!q || !k || !v || !out || !cu_q || !cu_kv || !prefix_len || !pack_len || !mask)
+    if (!q || !kv.k_pre || !kv.v_pre || !kv.k_pack || !kv.v_pack || !out || !cu_q || !prefix_len || !pack_len ||
+        !mask || (!kv.store && !cu_kv))
         return CAST_ERR_NULL_POINTER;
     const bool mfma = mfma_path(dtype, head_dim);
     if (!mfma && (head_dim > 128 || head_dim % 8)) return CAST_ERR_HEAD_DIM;
     const int64_t esz = dtype == CAST_BF16 ? 2 : 4;
+    int32_t max_rows = INT32_MAX;
     auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (mfma) {
-        if (!a16(q) || !a16(k) || !a16(v) || !a16(out)) return CAST_ERR_ALIGNMENT;
-        const int64_t strides[8] = {q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head};
+        if (!a16(q) || !a16(kv.k_pre) || !a16(kv.v_pre) || !a16(kv.k_pack) || !a16(kv.v_pack) || !a16(out))
+            return CAST_ERR_ALIGNMENT;
+        const int64_t strides[14] = {q_tok,     q_head,    kv.kpre_b,  kv.kpre_h,  kv.kpre_t,
+                                     kv.vpre_b, kv.vpre_h, kv.vpre_t,  kv.kpack_h, kv.kpack_t,
+                                     kv.vpack_h, kv.vpack_t, o_tok,    o_head};
         for (int64_t s : strides)
             if ((s * esz) % 16) return CAST_ERR_ALIGNMENT;
+        // key rows are addressed by 24-bit row index x 24-bit byte stride,
+        // within 2^31 bytes of their source's first row
+        const int64_t rows[4] = {kv.kpre_t, kv.vpre_t, kv.kpack_t, kv.vpack_t};
+        int64_t rb = 0;
+        for (int64_t r : rows) {
+            if (r < 0 || r * esz >= (int64_t)1 << 24) return CAST_ERR_SHAPE;
+            rb = r * esz > rb ? r * esz : rb;
+        }
+        const int64_t by_bytes = rb ? (((int64_t)1 << 31) - 1 - head_dim * esz) / rb : INT32_MAX;
+        const int64_t by_index = ((int64_t)1 << 24) - 64;
+        max_rows = (int32_t)(by_bytes < by_index ? by_bytes : by_index);
     }
-    (void)esz;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     AttnArgs a{};
     a.q = q;
-    a.k = k;
-    a.v = v;
+    a.kv = kv;
     a.out = out;
     a.lse = lse;
     a.cu_q = cu_q;
@@ -673,14 +834,11 @@ static int tree_attn_run(const void *q, const void *k, const void *v, void *out,
     a.G = num_q_heads / num_kv_heads;
     a.q_tok = q_tok;
     a.q_head = q_head;
-    a.k_tok = k_tok;
-    a.k_head = k_head;
-    a.v_tok = v_tok;
-    a.v_head = v_head;
     a.o_tok = o_tok;
     a.o_head = o_head;
     a.scale_log2 = sm_scale * kLog2e;
     a.status = status;
+    a.max_rows = max_rows;
 
     if (!mfma) {
         a.chunk = kNoSplit;
@@ -716,7 +874,9 @@ static int tree_attn_run(const void *q, const void *k, const void *v, void *out,
     int64_t items = (int64_t)num_kv_heads * rbmax * nsplit;
     items = (items + 7) & ~(int64_t)7;
     const unsigned grid = (unsigned)items;
-#define CAST_LAUNCH(DD, W) tree_attn_mfma_kernel<DD, W><<<grid, W * 64, 0, st>>>(a)
+#define CAST_LAUNCH(DD, W)                                                 \
+    (kv.store ? tree_attn_mfma_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
+              : tree_attn_mfma_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
     if (!(stages & kStageAttn)) {
     } else if (head_dim == 128) {
         if (waves == 2) CAST_LAUNCH(128, 2);
@@ -746,15 +906,61 @@ static int tree_attn_run(const void *q, const void *k, const void *v, void *out,
         int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head, int64_t k_tok, int64_t k_head, \
         int64_t v_tok, int64_t v_head, int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,         \
         int32_t kv_split, void *workspace, size_t workspace_bytes, int32_t *status, cast_stream_t stream
-#define CAST_ATTN_ARGS                                                                                        \
-    q, k, v, out, lse, cu_q, cu_kv, prefix_len, pack_len, mask, mask_words, batch, total_q, total_kv,        \
-        num_q_heads, num_kv_heads, head_dim, q_tok, q_head, k_tok, k_head, v_tok, v_head, o_tok, o_head,      \
-        dtype, sm_scale, kv_split, workspace, workspace_bytes, status, stream
 
-extern "C" int cast_tree_attn_fwd(CAST_ATTN_PARAMS) {
-    return tree_attn_run(CAST_ATTN_ARGS, kStageAttn | kStageCombine);
+static KvSource concat_source(const void *k, const void *v, int64_t k_tok, int64_t k_head, int64_t v_tok,
+                              int64_t v_head) {
+    KvSource s{};
+    s.k_pre = s.k_pack = k;
+    s.v_pre = s.v_pack = v;
+    s.kpre_t = s.kpack_t = k_tok;
+    s.kpre_h = s.kpack_h = k_head;
+    s.vpre_t = s.vpack_t = v_tok;
+    s.vpre_h = s.vpack_h = v_head;
+    s.store = 0;
+    return s;
 }
 
-extern "C" int cast_tree_attn_partial(CAST_ATTN_PARAMS) { return tree_attn_run(CAST_ATTN_ARGS, kStageAttn); }
+#define CAST_CONCAT_RUN(STAGES)                                                                                \
+    tree_attn_run(q, concat_source(k, v, k_tok, k_head, v_tok, v_head), out, lse, cu_q, cu_kv, prefix_len,  \
+                  pack_len, mask, mask_words, batch, total_q, total_kv, num_q_heads, num_kv_heads, head_dim,  \
+                  q_tok, q_head, o_tok, o_head, dtype, sm_scale, kv_split, workspace, workspace_bytes, status, \
+                  stream, STAGES)
 
-extern "C" int cast_tree_attn_combine(CAST_ATTN_PARAMS) { return tree_attn_run(CAST_ATTN_ARGS, kStageCombine); }
+extern "C" int cast_tree_attn_fwd(CAST_ATTN_PARAMS) { return CAST_CONCAT_RUN(kStageAttn | kStageCombine); }
+
+extern "C" int cast_tree_attn_partial(CAST_ATTN_PARAMS) { return CAST_CONCAT_RUN(kStageAttn); }
+
+extern "C" int cast_tree_attn_combine(CAST_ATTN_PARAMS) { return CAST_CONCAT_RUN(kStageCombine); }
+
+extern "C" int cast_tree_attn_store_fwd(const void *q, const void *k_store, const void *v_store, const void *k_pack,
+                                        const void *v_pack, void *out, float *lse, const int32_t *cu_q,
+                                        const int32_t *prefix_len, const int32_t *pack_len, const uint64_t *mask,
+                                        int32_t mask_words, int32_t batch, int32_t total_q, int32_t total_kv,
+                                        int32_t store_cap, int32_t num_q_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int64_t q_tok, int64_t q_head, int64_t ks_batch,
+                                        int64_t ks_head, int64_t ks_tok, int64_t vs_batch, int64_t vs_head,
+                                        int64_t vs_tok, int64_t kp_tok, int64_t kp_head, int64_t vp_tok,
+                                        int64_t vp_head, int64_t o_tok, int64_t o_head, int32_t dtype,
+                                        float sm_scale, int32_t kv_split, void *workspace, size_t workspace_bytes,
+                                        int32_t *status, cast_stream_t stream) {
+    KvSource s{};
+    s.k_pre = k_store;
+    s.v_pre = v_store;
+    s.k_pack = k_pack;
+    s.v_pack = v_pack;
+    s.kpre_b = ks_batch;
+    s.kpre_h = ks_head;
+    s.kpre_t = ks_tok;
+    s.vpre_b = vs_batch;
+    s.vpre_h = vs_head;
+    s.vpre_t = vs_tok;
+    s.kpack_t = kp_tok;
+    s.kpack_h = kp_head;
+    s.vpack_t = vp_tok;
+    s.vpack_h = vp_head;
+    s.store = 1;
+    s.cap = store_cap;
+    return tree_attn_run(q, s, out, lse, cu_q, nullptr, prefix_len, pack_len, mask, mask_words, batch, total_q,
+                         total_kv, num_q_heads, num_kv_heads, head_dim, q_tok, q_head, o_tok, o_head, dtype,
+                         sm_scale, kv_split, workspace, workspace_bytes, status, stream, kStageAttn | kStageCombine);
+}

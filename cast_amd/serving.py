@@ -1,0 +1,158 @@
+"""The verify pass's attention hook, reading the per-request KV store in place.
+
+Mirrors the attention side of cast_trees/serving.py:
+
+  VarlenPlan / PLAN   state of one ragged verify pass (serving.py:30-44),
+                      read by the hook once per layer
+  PACK_KV             the pass's post-RoPE pack K/V of every layer
+                      (serving.py:45), for the caller's accepted-path append
+  _varlen_attention   the HF AttentionInterface callee (serving.py:48-72),
+                      registered as "cast_varlen" (serving.py:75) when
+                      transformers is importable
+  begin_verify        the packing half of BatchedServer._verify_varlen
+                      (serving.py:208-253): packed tokens, positions,
+                      offsets and ancestor words, then PLAN.set
+
+The reference hook assembles a ragged [total_kv, Hkv, D] K/V per layer by
+gathering every request's prefix out of the store and scattering the pack
+behind it, up-casts all of it to fp32, and only then calls the attention
+(serving.py:61-71).  Here the kernel reads the prefix where it lies in
+buf_k/buf_v [B, Hkv, cap, D] and the pack from the forward's own K/V, in the
+store's dtype (bf16 products are exact in the fp32 MFMA accumulators, so the
+up-cast adds no precision to the score dot products; the probabilities are
+rounded to bf16 before the value product, as the reference kernel does for
+bf16 inputs, tree_attn.py:66,87).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .tree import MAX_PACK
+from .tree_attn import store_tree_attention
+from .verify import tree_bitmask
+
+
+class VarlenPlan:
+    """State of one ragged verify pass, read by the attention hook below."""
+    active = False
+
+    def set(self, **kw):
+        self.__dict__.update(kw)
+        self.layer = 0
+        self.active = True
+
+    def clear(self):
+        self.active = False
+        self.buf_k = self.buf_v = None
+        self.workspace = None
+
+
+PLAN = VarlenPlan()
+PACK_KV = {"k": [], "v": []}    # post-RoPE pack K/V of every layer, filled during the pass
+
+
+def _varlen_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
+    """HF attention callee: query [1, Hq, total_q, D], key/value [1, Hkv, total_q, D]
+    -> ([1, total_q, Hq, D], None)."""
+    if not PLAN.active:
+        # prefill and any other forward: plain SDPA (cast_trees/serving.py:49-55)
+        mask = attention_mask if not isinstance(attention_mask, bool) else None
+        o = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling,
+                                           is_causal=mask is None and query.shape[2] > 1, enable_gqa=True)
+        return o.transpose(1, 2).contiguous(), None
+
+    li = PLAN.layer
+    PLAN.layer += 1
+    while len(PACK_KV["k"]) <= li:
+        PACK_KV["k"].append(None)
+        PACK_KV["v"].append(None)
+    PACK_KV["k"][li], PACK_KV["v"][li] = key[0], value[0]
+    buf_k, buf_v = PLAN.buf_k[li], PLAN.buf_v[li]
+    q = query[0].transpose(0, 1)                          # [total_q, Hq, D] view
+    dt = buf_k.dtype
+    k_pack, v_pack = key[0], value[0]
+    if q.dtype != dt:
+        q = q.to(dt)
+    if k_pack.dtype != dt:
+        k_pack, v_pack = k_pack.to(dt), v_pack.to(dt)
+    if getattr(PLAN, "workspace", None) is None:
+        # split-K scratch, sized once per pass and shared by every layer
+        PLAN.workspace = torch.empty(max(workspace_bytes(q, buf_k, PLAN.total_kv), 256), dtype=torch.uint8,
+                                     device=q.device)
+    out = store_tree_attention(q, buf_k, buf_v, k_pack, v_pack, PLAN.cu_q, PLAN.prefix_len, PLAN.pack_len,
+                               PLAN.ancestor_mask, sm_scale=scaling, total_kv=PLAN.total_kv,
+                               workspace=PLAN.workspace)
+    return out.to(query.dtype).unsqueeze(0), None
+
+
+def workspace_bytes(q, buf_k, total_kv):
+    """Split-K workspace of one layer call with these shapes."""
+    from . import _lib
+    from .tree_attn import _DTYPES
+    B, H_kv = int(buf_k.shape[0]), int(buf_k.shape[1])
+    total_q, H_q, D = q.shape
+    return int(_lib.load().cast_tree_attn_workspace_size(B, total_q, int(total_kv), H_q, H_kv, D,
+                                                         _DTYPES[buf_k.dtype], 0))
+
+
+def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
+    """Pack B trees for one verify forward and activate the hook.
+
+    buf_k / buf_v: per-layer stores [B, Hkv, cap, D]; store_len[b]: tokens of
+    request b in the store; roots[b]: the root token (last committed token);
+    trees[b]: its TreeNode list; seq_lens[b]: the root's position.  Returns
+    (input_ids [1, total_q], position_ids [1, total_q], cu_q list), the inputs
+    of the target forward, which runs with ``_attn_implementation =
+    "cast_varlen"``; call ``PLAN.clear()`` afterwards (serving.py:244-253).
+    """
+    dev = torch.device(device) if device is not None else buf_k[0].device
+    B = len(trees)
+    pack_len = [1 + len(t) for t in trees]
+    if max(pack_len) > MAX_PACK:
+        raise ValueError(f"a pack holds at most {MAX_PACK} tokens (root + {MAX_PACK - 1} nodes)")
+    cap = int(buf_k[0].shape[2])
+    if max(store_len) > cap:
+        raise ValueError("store_len exceeds the store capacity")
+    tok, pos, parent = [], [], []
+    for b, nodes in enumerate(trees):
+        tok.append(int(roots[b]))
+        pos.append(int(seq_lens[b]))
+        parent.append(-1)
+        for nd in nodes:
+            tok.append(int(nd.token))
+            pos.append(int(seq_lens[b]) + int(nd.depth))
+            parent.append(int(nd.parent) + 1)
+    cu_q = [0]
+    for p in pack_len:
+        cu_q.append(cu_q[-1] + p)
+    total_q = cu_q[-1]
+    # one host-to-device copy for all int32 metadata
+    meta = torch.from_numpy(np.asarray(cu_q + list(store_len) + pack_len + parent, dtype=np.int32)).to(dev)
+    cu_q_t = meta[:B + 1]
+    prefix_t = meta[B + 1:2 * B + 1]
+    pack_t = meta[2 * B + 1:3 * B + 1]
+    parent_t = meta[3 * B + 1:]
+    words = tree_bitmask(parent_t, cu_q_t, 2)
+    n_layers = len(buf_k)
+    PACK_KV["k"], PACK_KV["v"] = [None] * n_layers, [None] * n_layers
+    PLAN.set(buf_k=buf_k, buf_v=buf_v, prefix_len=prefix_t, pack_len=pack_t, cu_q=cu_q_t,
+             total_kv=int(sum(store_len)) + total_q, ancestor_mask=words, parent=parent_t, workspace=None)
+    ids = torch.tensor([tok], dtype=torch.long, device=dev)
+    pos_ids = torch.tensor([pos], dtype=torch.long, device=dev)
+    return ids, pos_ids, cu_q
+
+
+def register():
+    """Register ``_varlen_attention`` as HF attention implementation "cast_varlen"
+    (cast_trees/serving.py:75).  Returns False when transformers is absent."""
+    try:
+        from transformers import AttentionInterface
+    except ImportError:
+        return False
+    AttentionInterface.register("cast_varlen", _varlen_attention)
+    return True
+
+
+register()

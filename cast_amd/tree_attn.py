@@ -143,3 +143,79 @@ def varlen_tree_attention(q, k, v, cu_q, cu_kv, prefix_len, pack_len, ancestor_m
     if check:
         _lib.raise_device_flags(status.item(), "varlen_tree_attention")
     return (out, lse) if return_lse else out
+
+
+def store_tree_attention(q, k_store, v_store, k_pack, v_pack, cu_q, prefix_len, pack_len, ancestor_mask,
+                         sm_scale=None, *, total_kv=None, return_lse=False, kv_split=0, check=False, out=None,
+                         workspace=None):
+    """Tree-verification attention reading the prefix K/V where it is stored.
+
+    The same attention as ``varlen_tree_attention``, but request b's keys are
+    its first S_b = prefix_len[b] store slots followed by its pack, with no
+    ragged K/V assembled (cast_trees/serving.py:61-68 copies both into one
+    tensor per layer):
+
+      q                [total_q, H_q, D]  (any token/head strides)
+      k_store/v_store  [B, H_kv, cap, D]  per-request store (serving.py:191-205)
+      k_pack/v_pack    [H_kv, total_q, D] the pass's own K/V, pack token j of
+                       request b at index cu_q[b] + j (HF's key[0] / value[0])
+      total_kv         host bound on sum(S_b + P_b) used to size the launch and
+                       workspace (default B*cap + total_q, always valid)
+
+    Returns ``out`` [total_q, H_q, D] (and ``lse`` with ``return_lse``).
+    """
+    lib = _lib.load()
+    total_q, H_q, D = q.shape
+    if k_store.dim() != 4 or k_pack.dim() != 3:
+        raise ValueError("k_store must be [B, H_kv, cap, D] and k_pack [H_kv, total_q, D]")
+    B, H_kv, cap = int(k_store.shape[0]), int(k_store.shape[1]), int(k_store.shape[2])
+    assert H_q % H_kv == 0
+    if not q.is_cuda:
+        raise ValueError("store_tree_attention runs on the GPU: tensors must be on the device")
+    if tuple(v_store.shape) != tuple(k_store.shape) or k_store.shape[3] != D:
+        raise ValueError("k_store and v_store must both be [B, H_kv, cap, D] with the head dim of q")
+    if tuple(k_pack.shape) != (H_kv, total_q, D) or tuple(v_pack.shape) != (H_kv, total_q, D):
+        raise ValueError(f"k_pack/v_pack must be [{H_kv}, {total_q}, {D}]")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {q.dtype}: use bfloat16 or float32")
+    if any(t.dtype != q.dtype for t in (k_store, v_store, k_pack, v_pack)):
+        raise ValueError("q, the store and the pack K/V must share one dtype (the store is read in place)")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    esz = q.element_size()
+    dev = q.device
+    q, k_pack, v_pack = _ready(q, esz), _ready(k_pack, esz), _ready(v_pack, esz)
+    if _ready(k_store, esz) is not k_store or _ready(v_store, esz) is not v_store:
+        raise ValueError("the store needs a contiguous head dim and 16-byte aligned strides")
+    cu_q = _as_i32(cu_q, dev)
+    prefix_len = _as_i32(prefix_len, dev)
+    pack_len = _as_i32(pack_len, dev)
+    if cu_q.shape[0] != B + 1 or prefix_len.shape[0] != B or pack_len.shape[0] != B:
+        raise ValueError("cu_q needs B+1 entries and prefix_len / pack_len B entries (B = store batch)")
+    if total_kv is None:
+        total_kv = B * cap + total_q
+    total_kv = int(total_kv)
+    mask, words = _mask_words(ancestor_mask, total_q, dev)
+    if out is None:
+        out = torch.empty((total_q, H_q, D), dtype=q.dtype, device=dev)
+    elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with a contiguous head dim")
+    lse = torch.empty((total_q, H_q), dtype=torch.float32, device=dev) if return_lse else None
+    dt = _DTYPES[q.dtype]
+    ws_bytes = lib.cast_tree_attn_workspace_size(B, total_q, total_kv, H_q, H_kv, D, dt, kv_split)
+    if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
+    with torch.cuda.device(dev):
+        st = lib.cast_tree_attn_store_fwd(
+            _lib.ptr(q), _lib.ptr(k_store), _lib.ptr(v_store), _lib.ptr(k_pack), _lib.ptr(v_pack), _lib.ptr(out),
+            _lib.ptr(lse), _lib.ptr(cu_q), _lib.ptr(prefix_len), _lib.ptr(pack_len), _lib.ptr(mask), words,
+            B, total_q, total_kv, cap, H_q, H_kv, D, q.stride(0), q.stride(1),
+            k_store.stride(0), k_store.stride(1), k_store.stride(2), v_store.stride(0), v_store.stride(1),
+            v_store.stride(2), k_pack.stride(1), k_pack.stride(0), v_pack.stride(1), v_pack.stride(0),
+            out.stride(0), out.stride(1), dt, float(sm_scale), int(kv_split),
+            _lib.ptr(workspace) if ws_bytes else None, ws_bytes, _lib.ptr(status), _lib.stream_of(q))
+    _lib.check(st, "cast_tree_attn_store_fwd")
+    if check:
+        _lib.raise_device_flags(status.item(), "store_tree_attention")
+    return (out, lse) if return_lse else out

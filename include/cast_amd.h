@@ -46,7 +46,10 @@ enum cast_status {
 enum cast_device_flag {
     CAST_FLAG_BAD_PACK = 1,        /* pack_len outside [1, 128] or beyond the mask words */
     CAST_FLAG_BAD_OFFSETS = 2,     /* cu_q / cu_kv / prefix_len inconsistent with totals */
-    CAST_FLAG_BAD_PARENT = 4       /* a parent index not in [-1, own index) */
+    CAST_FLAG_BAD_PARENT = 4,      /* a parent index not in [-1, own index) */
+    CAST_FLAG_TOO_LONG = 8         /* a request's key source exceeds the kernel's
+                                      row addressing (bf16 MFMA path: 2^24 - 64
+                                      rows and 2^31 bytes per source) */
 };
 
 enum cast_dtype { CAST_BF16 = 0, CAST_FP32 = 1 };
@@ -129,6 +132,37 @@ int cast_tree_attn_combine(const void *q, const void *k, const void *v, void *ou
                            int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,
                            int32_t kv_split, void *workspace, size_t workspace_bytes,
                            int32_t *status, cast_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * K2 over a per-request KV store, read in place.
+ * Replaces the per-layer ragged K/V assembly of the reference attention hook
+ * (cast_trees/serving.py:61-68: prefix gathered out of buf_k/buf_v
+ * [B, Hkv, cap, D], pack scattered behind it, both up-cast to fp32) and the
+ * call it feeds (serving.py:69-71 -> cast_trees/tree_attn.py:116-139).
+ * Request b's keys are its S_b = prefix_len[b] stored tokens followed by its
+ * P_b pack tokens; nothing is copied:
+ *   k_store, v_store  prefix key t of request b, head h at
+ *                     base + b*ks_batch + h*ks_head + t*ks_tok (elements);
+ *                     S_b <= store_cap is checked on the device
+ *   k_pack, v_pack    pack key j of request b, head h at
+ *                     base + (cu_q[b] + j)*kp_tok + h*kp_head, i.e. the
+ *                     forward's own K/V [Hkv, total_q, D] in any strides
+ *   total_kv          a bound on sum_b (S_b + P_b) (sizes grid and workspace;
+ *                     a batch above it is flagged CAST_FLAG_BAD_OFFSETS)
+ * Every other argument and the output are as in cast_tree_attn_fwd; the
+ * workspace is cast_tree_attn_workspace_size(batch, total_q, total_kv, ...).
+ * ------------------------------------------------------------------- */
+int cast_tree_attn_store_fwd(const void *q, const void *k_store, const void *v_store,
+                             const void *k_pack, const void *v_pack, void *out, float *lse,
+                             const int32_t *cu_q, const int32_t *prefix_len, const int32_t *pack_len,
+                             const uint64_t *mask, int32_t mask_words, int32_t batch, int32_t total_q,
+                             int32_t total_kv, int32_t store_cap, int32_t num_q_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
+                             int64_t ks_batch, int64_t ks_head, int64_t ks_tok, int64_t vs_batch,
+                             int64_t vs_head, int64_t vs_tok, int64_t kp_tok, int64_t kp_head,
+                             int64_t vp_tok, int64_t vp_head, int64_t o_tok, int64_t o_head,
+                             int32_t dtype, float sm_scale, int32_t kv_split, void *workspace,
+                             size_t workspace_bytes, int32_t *status, cast_stream_t stream);
 
 /* Workspace bytes cast_tree_attn_fwd needs for these host-known sizes. */
 size_t cast_tree_attn_workspace_size(int32_t batch, int32_t total_q, int32_t total_kv,

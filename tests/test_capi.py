@@ -27,7 +27,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert names == sorted(_lib.SIGNATURES), "ctypes bindings and header disagree"
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.cast_abi_version() == 1
+    assert lib.cast_abi_version() == 2
 
 
 def test_status_strings(lib):
@@ -88,3 +88,21 @@ def test_python_layer_maps_errors():
     with pytest.raises(ValueError):
         _lib.raise_device_flags(_lib.FLAG_BAD_PARENT, "x")
     _lib.raise_device_flags(0, "x")
+
+
+def _store(lib, **over):
+    a = dict(ptrs=[None] * 11, words=2, B=1, tq=16, tkv=32, cap=64, Hq=32, Hkv=8, D=128, strides=[8] * 14,
+             dtype=0, scale=0.1, split=0, ws=None, wsb=0, status=None, stream=None)
+    a.update(over)
+    return lib.cast_tree_attn_store_fwd(*a["ptrs"], a["words"], a["B"], a["tq"], a["tkv"], a["cap"], a["Hq"],
+                                        a["Hkv"], a["D"], *a["strides"], a["dtype"], a["scale"], a["split"],
+                                        a["ws"], a["wsb"], a["status"], a["stream"])
+
+
+def test_store_attention_host_validation(lib):
+    assert _store(lib) == 1                              # null pointers
+    assert _store(lib, Hkv=3) == 2                       # head ratio
+    assert _store(lib, cap=-1) == 7                      # negative capacity
+    assert _store(lib, dtype=2) == 4
+    assert _store(lib, scale=-1.0) == 9
+    assert _store(lib, B=0) == 0                         # nothing to do
