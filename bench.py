@@ -144,6 +144,60 @@ def cpu_baseline(wl, budget_s=12.0):
                        f"({med * 1e3:.1f} ms each), scaled x{wl.B}")
 
 
+def store_layout(dev, steps, warmup):
+    """The attention hook's per-layer work on the headline shapes, prefix in a
+    per-request store [B, Hkv, cap, D] (cap = S + 320) and the pack as HF
+    hands it over ([Hkv, total_q, D]): the in-place call vs assembling the
+    ragged K/V first, as cast_trees/serving.py:61-66 does (gather + scatter;
+    the reference's fp32 up-cast on top is not included)."""
+    import torch
+    from cast_amd import scenarios
+    from cast_amd.tree_attn import store_tree_attention
+    from cast_amd import tree_bitmask, varlen_tree_attention
+    wl = scenarios.qwen3_headline()
+    meta = wl.meta_tensors(dev)
+    mask = tree_bitmask(meta["parent"], meta["cu_q"], 2)
+    B, Hkv, D, S = wl.B, wl.Hkv, wl.D, int(wl.prefix_len[0])
+    cap = S + 320
+    g = torch.Generator(device=dev).manual_seed(5)
+    kst = torch.randn((B, Hkv, cap, D), generator=g, device=dev).to(torch.bfloat16)
+    vst = torch.randn((B, Hkv, cap, D), generator=g, device=dev).to(torch.bfloat16)
+    kpk = torch.randn((wl.total_q, Hkv, D), generator=g, device=dev).to(torch.bfloat16).transpose(0, 1)
+    vpk = torch.randn((wl.total_q, Hkv, D), generator=g, device=dev).to(torch.bfloat16).transpose(0, 1)
+    q = torch.randn((wl.Hq, wl.total_q, D), generator=g, device=dev).to(torch.bfloat16).transpose(0, 1)
+    total_kv = wl.total_kv
+    ws = torch.empty(1 << 27, dtype=torch.uint8, device=dev)
+    # the reference's gather / scatter indices (serving.py:234-240)
+    pl = torch.from_numpy(wl.prefix_len.astype("int64")).to(dev)
+    cu_kv = meta["cu_kv"].long()
+    pre_b = torch.repeat_interleave(torch.arange(B, device=dev), pl)
+    cu_pre = torch.cat([pl.new_zeros(1), pl.cumsum(0)])
+    pre_pos = torch.arange(int(cu_pre[-1]), device=dev) - cu_pre[:-1].repeat_interleave(pl)
+    pre_dst = cu_kv[:-1].repeat_interleave(pl) + pre_pos
+    pkl = torch.from_numpy(wl.pack_len.astype("int64")).to(dev)
+    within = torch.arange(wl.total_q, device=dev) - meta["cu_q"].long()[:-1].repeat_interleave(pkl)
+    pack_dst = (cu_kv[:-1] + pl).repeat_interleave(pkl) + within
+
+    def inplace():
+        store_tree_attention(q, kst, vst, kpk, vpk, meta["cu_q"], meta["prefix_len"], meta["pack_len"], mask,
+                             total_kv=total_kv, workspace=ws)
+
+    def assembled():
+        k_rag = torch.empty((total_kv, Hkv, D), dtype=torch.bfloat16, device=dev)
+        v_rag = torch.empty_like(k_rag)
+        k_rag[pre_dst] = kst[pre_b, :, pre_pos, :]
+        v_rag[pre_dst] = vst[pre_b, :, pre_pos, :]
+        k_rag[pack_dst] = kpk.transpose(0, 1)
+        v_rag[pack_dst] = vpk.transpose(0, 1)
+        varlen_tree_attention(q, k_rag, v_rag, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                              mask, workspace=ws)
+
+    t_in = time_kernel(inplace, steps, warmup)
+    t_as = time_kernel(assembled, steps, warmup)
+    log(f"  store layout: in place {t_in:.1f} us/call, ragged assembly + attention {t_as:.1f} us/call")
+    return dict(inplace_us=round(t_in, 2), assembled_us=round(t_as, 2), cap=cap)
+
+
 def secondary(dev, steps, warmup):
     import torch
     from cast_amd import greedy_accept, scenarios, tree_bitmask
@@ -161,6 +215,7 @@ def secondary(dev, steps, warmup):
             f"{rl['bound']} frac {rl['frac']:.3f}")
         del h
         torch.cuda.empty_cache()
+    res["store_layout"] = store_layout(dev, steps, warmup)
     # K1 and K3 on the headline trees, full Qwen3 vocabulary logits
     wl = scenarios.qwen3_headline()
     meta = wl.meta_tensors(dev)
