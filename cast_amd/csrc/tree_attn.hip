@@ -77,9 +77,11 @@ struct AttnArgs {
 struct Seq {
     int b, S, P, T, q0, kv0, ns, rb, split_len;
     int64_t part_off;   // first partial row of this request (only if ns > 1)
+    int64_t unit_off;   // first (KV head, row block) unit of this request
 };
 
-__device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s) {
+// Reads and checks request b's metadata; `report` raises the device flags.
+__device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s, bool report) {
     const int S = a.prefix_len[b], P = a.pack_len[b];
     const int q0 = a.cu_q[b], q1 = a.cu_q[b + 1];
     int kv0 = 0, kv1 = S + P;
@@ -92,15 +94,15 @@ __device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s) {
         bad_kv = kv0 < 0 || kv1 > a.total_kv || kv1 - kv0 != S + P;
     }
     if ((a.kv.store ? max(S, P) : S + P) > a.max_rows) {
-        if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_TOO_LONG);
+        if (report) raise_flag(a.status, CAST_FLAG_TOO_LONG);
         return false;
     }
     if (S < 0 || q0 < 0 || q1 > a.total_q || q1 - q0 != P || bad_kv) {
-        if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        if (report) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         return false;
     }
     if (P < 0 || P > 64 * a.mask_words) {
-        if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_BAD_PACK);
+        if (report) raise_flag(a.status, CAST_FLAG_BAD_PACK);
         return false;
     }
     s.b = b;
@@ -116,8 +118,62 @@ __device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s) {
     return true;
 }
 
-// Total work items and, for item w, the request and in-request index.
-// Items are ordered (b, h, split, row block) with the row block fastest.
+// ---- batch lookups.  A wave walks the batch 64 requests at a time, lane j
+// holding request b0 + j, with wave prefix sums over the lanes, so that a
+// lookup costs one round of metadata loads per 64 requests.
+
+__device__ __forceinline__ int64_t shfl64(int64_t x, int src) {
+    const int lo = __shfl((int)(uint32_t)x, src), hi = __shfl((int)(x >> 32), src);
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+// lane src's value in every lane, as a scalar (src wave-uniform)
+__device__ __forceinline__ int bcast(int x, int src) { return __builtin_amdgcn_readlane(x, src); }
+__device__ __forceinline__ int64_t bcast64(int64_t x, int src) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, src);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(x >> 32), src);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int64_t wave_scan(int64_t x) {   // inclusive
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t y = shfl64(x, lane >= off ? lane - off : lane);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+__device__ __forceinline__ Seq shfl_seq(const Seq &t, int src) {
+    Seq s;
+    s.b = bcast(t.b, src);
+    s.S = bcast(t.S, src);
+    s.P = bcast(t.P, src);
+    s.T = bcast(t.T, src);
+    s.q0 = bcast(t.q0, src);
+    s.kv0 = bcast(t.kv0, src);
+    s.ns = bcast(t.ns, src);
+    s.rb = bcast(t.rb, src);
+    s.split_len = bcast(t.split_len, src);
+    return s;
+}
+
+// Work items are ordered (b, h, split, row block) with the row block fastest.
+__device__ __forceinline__ int64_t items_of(const AttnArgs &a, const Seq &t) { return (int64_t)a.Hkv * t.ns * t.rb; }
+
+// Total work items and key rows of the valid requests.  Wave 0 of the
+// workgroup reports invalid requests.
+__device__ void batch_totals(const AttnArgs &a, int64_t &items, int64_t &kv_sum) {
+    const int lane = threadIdx.x & 63;
+    items = 0;
+    kv_sum = 0;
+    for (int b0 = 0; b0 < a.batch; b0 += 64) {
+        const int b = b0 + lane;
+        Seq t;
+        const bool ok = b < a.batch && load_seq(a, b, t, threadIdx.x < 64);
+        items += bcast64(wave_scan(ok ? items_of(a, t) : 0), 63);
+        kv_sum += bcast64(wave_scan(ok ? t.T : 0), 63);
+    }
+}
+
 // In the store layout total_kv is a caller-supplied bound on sum(S_b + P_b)
 // that sized the grid and the workspace; a batch exceeding it is rejected
 // whole.  (The concat layout checks every request against it in load_seq.)
@@ -129,29 +185,36 @@ __device__ __forceinline__ bool store_total_ok(const AttnArgs &a, int64_t kv_sum
     return true;
 }
 
-__device__ bool find_item(const AttnArgs &a, int w, Seq &s, int &local, int &total) {
-    total = 0;
-    bool found = false;
-    int64_t part = 0, kv_sum = 0;
-    for (int b = 0; b < a.batch; ++b) {
+// The request holding work item w (or, with by_token, packed row w), with its
+// first partial row and first (KV head, row block) unit; local = w's index
+// within the request.  Wave-uniform result.
+__device__ bool find_request(const AttnArgs &a, int64_t w, bool by_token, Seq &s, int &local) {
+    const int lane = threadIdx.x & 63;
+    int64_t items = 0, part = 0, units = 0;
+    for (int b0 = 0; b0 < a.batch; b0 += 64) {
+        const int b = b0 + lane;
         Seq t;
-        if (!load_seq(a, b, t)) continue;
-        const int n = a.Hkv * t.ns * t.rb;
-        if (!found && w >= total && w < total + n) {
-            s = t;
-            s.part_off = part;
-            local = w - total;
-            found = true;
+        const bool ok = b < a.batch && load_seq(a, b, t, false);
+        const int64_t n = ok ? items_of(a, t) : 0;
+        const int64_t pp = ok && t.ns > 1 ? (int64_t)t.ns * t.P : 0;
+        const int64_t uu = ok ? (int64_t)a.Hkv * t.rb : 0;
+        const int64_t n_in = wave_scan(n), p_in = wave_scan(pp), u_in = wave_scan(uu);
+        const int64_t start = by_token ? (ok ? t.q0 : 0) : items + n_in - n;
+        const int64_t len = by_token ? (ok ? t.P : 0) : n;
+        const uint64_t hit = __ballot(ok && w >= start && w < start + len);
+        if (hit) {
+            const int src = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
+            s = shfl_seq(t, src);
+            s.part_off = part + bcast64(p_in - pp, src);
+            s.unit_off = units + bcast64(u_in - uu, src);
+            local = (int)(w - bcast64(start, src));
+            return true;
         }
-        total += n;
-        kv_sum += t.T;
-        if (t.ns > 1) part += (int64_t)t.ns * t.P;
+        items += bcast64(n_in, 63);
+        part += bcast64(p_in, 63);
+        units += bcast64(u_in, 63);
     }
-    if (!store_total_ok(a, kv_sum)) {
-        total = 0;
-        return false;
-    }
-    return found;
+    return false;
 }
 
 // Base pointers and token strides of the prefix and pack keys of one
@@ -264,18 +327,17 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     // consecutive items (the row blocks of one key split) run on one XCD
     // (workgroups are dealt to the 8 XCDs round-robin) and share its L2.
     Seq sq;
-    int local, total;
+    int local;
     {
-        Seq dummy;
-        int l0;
-        find_item(a, -1, dummy, l0, total);
-        const int n8 = (total + 7) & ~7;
-        const int x = blockIdx.x;
+        int64_t total, kv_sum;
+        batch_totals(a, total, kv_sum);
+        if (!store_total_ok(a, kv_sum)) return;
+        const int64_t n8 = (total + 7) & ~(int64_t)7;
+        const int64_t x = blockIdx.x;
         if (x >= n8) return;
-        const int w = (x & 7) * (n8 >> 3) + (x >> 3);
+        const int64_t w = (x & 7) * (n8 >> 3) + (x >> 3);
         if (w >= total) return;
-        int t2;
-        if (!find_item(a, w, sq, local, t2)) return;
+        if (!find_request(a, w, false, sq, local)) return;
     }
     const int rb = local % sq.rb;
     const int split = (local / sq.rb) % sq.ns;
@@ -559,23 +621,13 @@ template <typename OutT, int D>
 __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     const int tok = blockIdx.x;
     Seq sq;
-    bool found = false;
-    int64_t part = 0, kv_sum = 0;
-    // the store layout checks the whole batch against its total_kv bound;
-    // the concat layout can stop at its own request
-    for (int b = 0; b < a.batch && !(found && !a.kv.store); ++b) {
-        Seq t;
-        if (!load_seq(a, b, t)) continue;
-        if (!found && tok >= t.q0 && tok < t.q0 + t.P) {
-            sq = t;
-            sq.part_off = part;
-            found = true;
-        }
-        kv_sum += t.T;
-        if (t.ns > 1) part += (int64_t)t.ns * t.P;
+    int i;
+    if (a.kv.store) {
+        int64_t items, kv_sum;
+        batch_totals(a, items, kv_sum);
+        if (!store_total_ok(a, kv_sum)) return;
     }
-    if (!store_total_ok(a, kv_sum) || !found || sq.ns <= 1) return;
-    const int i = tok - sq.q0;
+    if (!find_request(a, tok, true, sq, i) || sq.ns <= 1) return;
     if (sq.part_off + (int64_t)sq.ns * sq.P > a.part_rows) return;
     constexpr int C = D / 4;
     for (int c = threadIdx.x; c < a.Hq * C; c += blockDim.x) {
@@ -627,8 +679,13 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
 
     // items: (b, h, 16-row block); rows_wg == 16 for this kernel
     Seq sq;
-    int local, total;
-    if (!find_item(a, blockIdx.x, sq, local, total)) return;
+    int local;
+    {
+        int64_t total, kv_sum;
+        batch_totals(a, total, kv_sum);
+        if (!store_total_ok(a, kv_sum)) return;
+        if (!find_request(a, blockIdx.x, false, sq, local)) return;
+    }
     const int rb = local % sq.rb;
     const int h = local / (sq.rb * sq.ns);
     const int rows = sq.P * a.G;
