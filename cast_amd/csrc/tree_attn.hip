@@ -67,6 +67,7 @@ struct AttnArgs {
     int32_t chunk;      // keys per split, multiple of 64 (kNoSplit = no split)
     int32_t max_rows;   // longest key source (rows) the MFMA kernel can address
     int32_t rows_wg;    // query rows per workgroup
+    int32_t comb_groups;  // combine kernel: head groups per packed token
     float *part_o;      // [part_rows][Hq][D] fp32, normalised partial outputs
     float *part_lse;    // [part_rows][Hq]    fp32, base-2 partial lse
     int64_t part_rows;
@@ -617,9 +618,16 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 // --------------------------------------------------------------------------
 // Split-K combine: one workgroup per packed token, all query heads.
 // --------------------------------------------------------------------------
+// One workgroup per (packed token, group of query heads): a.comb_groups
+// groups of ceil(Hq / comb_groups) heads, each thread one 4-wide chunk of a
+// head's output at a time.
 template <typename OutT, int D>
 __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
-    const int tok = blockIdx.x;
+    constexpr int C = D / 4;
+    const int groups = a.comb_groups;
+    const int tok = blockIdx.x / groups;
+    const int hpg = (a.Hq + groups - 1) / groups;
+    const int h0 = (blockIdx.x % groups) * hpg;
     Seq sq;
     int i;
     if (a.kv.store) {
@@ -629,20 +637,23 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     }
     if (!find_request(a, tok, true, sq, i) || sq.ns <= 1) return;
     if (sq.part_off + (int64_t)sq.ns * sq.P > a.part_rows) return;
-    constexpr int C = D / 4;
-    for (int c = threadIdx.x; c < a.Hq * C; c += blockDim.x) {
-        const int hq = c / C, d4 = c % C;
+    const int64_t lstride = (int64_t)sq.P * a.Hq, xstride = lstride * D;
+    const int hend = min(a.Hq, h0 + hpg);
+    for (int c = threadIdx.x; c < (hend - h0) * C; c += 256) {
+        const int hq = h0 + c / C, d4 = c % C;
+        const float *lp = a.part_lse + (sq.part_off + i) * a.Hq + hq;   // split s at + s*lstride
+        const float *xp = a.part_o + ((sq.part_off + i) * a.Hq + hq) * D + d4 * 4;
         float M = -INFINITY;
-        for (int s = 0; s < sq.ns; ++s)
-            M = fmaxf(M, a.part_lse[(sq.part_off + (int64_t)s * sq.P + i) * a.Hq + hq]);
+#pragma unroll 4
+        for (int s = 0; s < sq.ns; ++s) M = fmaxf(M, lp[s * lstride]);
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
         float L = 0.f;
         if (M != -INFINITY) {
+#pragma unroll 4
             for (int s = 0; s < sq.ns; ++s) {
-                const int64_t prow = sq.part_off + (int64_t)s * sq.P + i;
-                const float w = exp2f(a.part_lse[prow * a.Hq + hq] - M);
+                const float w = exp2f(lp[s * lstride] - M);
                 L += w;
-                const floatx4 x = *reinterpret_cast<const floatx4 *>(a.part_o + (prow * a.Hq + hq) * D + d4 * 4);
+                const floatx4 x = *reinterpret_cast<const floatx4 *>(xp + s * xstride);
                 acc += w * x;
             }
             acc *= 1.f / L;
@@ -654,7 +665,8 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
         } else {
             *reinterpret_cast<floatx4 *>(op) = acc;
         }
-        if (a.lse && d4 == 0) a.lse[(int64_t)tok * a.Hq + hq] = M == -INFINITY ? -INFINITY : (M + log2f(L)) * kLn2;
+        if (a.lse && d4 == 0)
+            a.lse[(int64_t)tok * a.Hq + hq] = M == -INFINITY ? -INFINITY : (M + log2f(L)) * kLn2;
     }
 }
 
@@ -947,10 +959,15 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
 #undef CAST_LAUNCH
     if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     if (a.chunk != kNoSplit && (stages & kStageCombine)) {
+        // about 1536 workgroups (6 per CU), each with up to 256 output chunks
+        const int64_t max_groups = ((int64_t)num_q_heads * (head_dim / 4) + 255) / 256;
+        int64_t g = 1536 / total_q;
+        g = g < 1 ? 1 : (g > max_groups ? max_groups : g);
+        a.comb_groups = (int32_t)g;
         if (head_dim == 128)
-            tree_attn_combine_kernel<uint16_t, 128><<<total_q, 256, 0, st>>>(a);
+            tree_attn_combine_kernel<uint16_t, 128><<<(unsigned)(total_q * g), 256, 0, st>>>(a);
         else
-            tree_attn_combine_kernel<uint16_t, 64><<<total_q, 256, 0, st>>>(a);
+            tree_attn_combine_kernel<uint16_t, 64><<<(unsigned)(total_q * g), 256, 0, st>>>(a);
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     }
     return CAST_OK;
