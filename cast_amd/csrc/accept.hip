@@ -41,8 +41,16 @@ __global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict_
     const char *base = static_cast<const char *>(logits) + (size_t)row * (size_t)ld * esz;
     const bool vec = ((reinterpret_cast<uintptr_t>(base) & 15) == 0);
     const int nch = vec ? vocab / EPC : 0;
-    for (int c = tid; c < nch; c += NT) {
-        const u32x4 w = *reinterpret_cast<const u32x4 *>(base + (size_t)c * 16);
+    // A thread visits its elements in increasing index order, so an element
+    // replaces the running best iff it is the first, strictly greater, or the
+    // first NaN: ties keep the earlier index and a NaN best is never replaced.
+    // Branch-free (compares and selects only).
+    auto take = [&](float v, int i) {
+        const bool t = (v > best) | ((v != v) & (best == best));
+        best = t ? v : best;
+        bi = t ? i : bi;
+    };
+    auto scan_chunk = [&](const u32x4 &w, int c, bool first) {
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
             float v;
@@ -53,22 +61,41 @@ __global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict_
                 v = bf16_to_float((uint16_t)(bits >> ((e & 1) * 16)));
             else
                 v = __builtin_bit_cast(float, bits);
-            const int i = c * EPC + e;
-            if (better(v, i, best, bi)) {
+            if (first && e == 0) {   // the thread's first element seeds the running best
                 best = v;
-                bi = i;
+                bi = c * EPC;
+            } else {
+                take(v, c * EPC + e);
             }
         }
+    };
+    // UNR independent 16-byte loads in flight per thread, then the compares
+    // (in increasing index order per thread, as the tie rule needs)
+    constexpr int UNR = 4;
+    int c = tid;
+    if (c < nch) {
+        scan_chunk(*reinterpret_cast<const u32x4 *>(base + (size_t)c * 16), c, true);
+        c += NT;
     }
+    for (; c + (UNR - 1) * NT < nch; c += UNR * NT) {
+        u32x4 w[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c + u * NT) * 16);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) scan_chunk(w[u], c + u * NT, false);
+    }
+    for (; c < nch; c += NT) scan_chunk(*reinterpret_cast<const u32x4 *>(base + (size_t)c * 16), c, false);
     for (int i = nch * EPC + tid; i < vocab; i += NT) {
         float v;
         if constexpr (BF16)
             v = bf16_to_float(reinterpret_cast<const uint16_t *>(base)[i]);
         else
             v = reinterpret_cast<const float *>(base)[i];
-        if (better(v, i, best, bi)) {
+        if (bi == INT_MAX) {     // no vector chunk seeded this thread
             best = v;
             bi = i;
+        } else {
+            take(v, i);
         }
     }
 #pragma unroll
