@@ -12,6 +12,10 @@ Mirrors the attention side of cast_trees/serving.py:
   begin_verify        the packing half of BatchedServer._verify_varlen
                       (serving.py:208-253): packed tokens, positions,
                       offsets and ancestor words, then PLAN.set
+  _tree_attention     the batch-one verify of cast_trees/decode.py:166-171
+                      (target forward with the additive tree mask of
+                      cast_trees/verify.py:15-25) through the same kernel,
+                      registered as "cast_tree"
 
 The reference hook assembles a ragged [total_kv, Hkv, D] K/V per layer by
 gathering every request's prefix out of the store and scattering the pack
@@ -24,6 +28,8 @@ rounded to bf16 before the value product, as the reference kernel does for
 bf16 inputs, tree_attn.py:66,87).
 """
 from __future__ import annotations
+
+import weakref
 
 import numpy as np
 import torch
@@ -144,14 +150,75 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
     return ids, pos_ids, cu_q
 
 
+# ---- batch-one verify (cast_trees/decode.py:166-171): the target forward over
+# [root] + nodes with the additive tree mask of cast_trees/verify.py:15-25,
+# routed through the same kernel
+
+# the last mask seen (weak reference, so a new tensor never matches) with its
+# version and key length, and the kernel metadata derived from it
+_TREE_META = {"ref": None, "key": None, "meta": None}
+
+
+def _tree_meta(mask, n_kv):
+    """Kernel metadata for a (1, 1, n, S + n) additive tree mask, or None when
+    the mask is not one (a masked prefix key, or a pack longer than 128).  The
+    same mask object is handed to every layer of one forward: derived once."""
+    key = (None if mask.is_inference() else mask._version, n_kv)
+    ref = _TREE_META["ref"]
+    if ref is not None and ref() is mask and _TREE_META["key"] == key:
+        return _TREE_META["meta"]
+    n, width = int(mask.shape[-2]), int(mask.shape[-1])
+    S = width - n
+    if mask.dim() != 4 or mask.shape[0] != 1 or mask.shape[1] != 1 or S < 0 or width != n_kv or n > MAX_PACK:
+        return None
+    vis = mask[0, 0] == 0
+    if S and not bool(vis[:, :S].all()):
+        return None
+    tree = vis[:, S:].to(torch.int64)
+    j = torch.arange(n, device=mask.device)
+    bits = tree << (j % 64)
+    words = torch.zeros((n, 2), dtype=torch.int64, device=mask.device)
+    words[:, 0] = bits[:, :64].sum(dim=1)          # distinct bits: the sum is the OR
+    if n > 64:
+        words[:, 1] = bits[:, 64:].sum(dim=1)
+    meta = torch.tensor([0, n, 0, n_kv, S, n], dtype=torch.int32, device=mask.device)
+    out = (meta[0:2], meta[2:4], meta[4:5], meta[5:6], words)
+    _TREE_META.update(ref=weakref.ref(mask), key=key, meta=out)
+    return out
+
+
+def _tree_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
+    """HF attention callee for the batch-one tree verify pass: query [1, Hq, n, D],
+    key/value [1, Hkv, S + n, D] (the cache after its update), attention_mask the
+    (1, 1, n, S + n) additive tree mask -> ([1, n, Hq, D], None).  Anything else
+    (prefill, no mask, a non-tree mask) runs plain SDPA."""
+    meta = None
+    if (isinstance(attention_mask, torch.Tensor) and query.shape[0] == 1 and query.is_cuda
+            and query.dtype in (torch.bfloat16, torch.float32)):
+        meta = _tree_meta(attention_mask, int(key.shape[2]))
+    if meta is None:
+        mask = attention_mask if not isinstance(attention_mask, bool) else None
+        o = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling,
+                                           is_causal=mask is None and query.shape[2] > 1, enable_gqa=True)
+        return o.transpose(1, 2).contiguous(), None
+    from .tree_attn import varlen_tree_attention
+    cu_q, cu_kv, prefix_len, pack_len, words = meta
+    out = varlen_tree_attention(query[0].transpose(0, 1), key[0].transpose(0, 1), value[0].transpose(0, 1),
+                                cu_q, cu_kv, prefix_len, pack_len, words, sm_scale=scaling)
+    return out.unsqueeze(0), None
+
+
 def register():
-    """Register ``_varlen_attention`` as HF attention implementation "cast_varlen"
-    (cast_trees/serving.py:75).  Returns False when transformers is absent."""
+    """Register the HF attention implementations (cast_trees/serving.py:75):
+    "cast_varlen" (the batched verify over the KV store) and "cast_tree" (the
+    batch-one verify over a DynamicCache with the additive tree mask).
+    Returns False when transformers is absent."""
     try:
         from transformers import AttentionInterface
     except ImportError:
         return False
     AttentionInterface.register("cast_varlen", _varlen_attention)
+    AttentionInterface.register("cast_tree", _tree_attention)
     return True
 
 

@@ -195,3 +195,50 @@ def test_hf_hook_matches_dense_batch_one_path(gpu):
         print(f"  request {b}: logits max |diff| {err:.3e} (scale {scale:.2f})", flush=True)
         assert err <= 2e-2 * scale
         assert OW.greedy_walk(nodes, g.cpu()) == OW.greedy_walk(nodes, w.cpu())
+
+
+@torch.inference_mode()
+def test_hf_batch_one_tree_hook_matches_sdpa(gpu):
+    # cast_trees/decode.py:166-171: the target forward over [root] + nodes with
+    # past_key_values = the prefix cache and the additive tree mask, here with
+    # attn "cast_tree" (the tree kernel, K/V read from the cache in place) vs
+    # "sdpa" on an identical cache
+    import copy
+    transformers = pytest.importorskip("transformers")
+    from cast_amd import serving, tree as T
+    from cast_amd.verify import tree_attention_mask
+    from oracle import walk as OW
+    assert serving.register()
+    model = _tiny_qwen3(gpu)
+    V = model.config.vocab_size
+    rng = np.random.default_rng(11)
+    for S, budget in ((77, 15), (300, 63), (1030, 127)):
+        print(f"case hf-tree-hook: prefix {S}, nodes {budget}", flush=True)
+        prompt = torch.from_numpy(rng.integers(0, V, size=S)).to(gpu)
+        cache = transformers.DynamicCache()
+        model(prompt[None], past_key_values=cache, use_cache=True)
+        top_idx, top_lp = T.block_topk(rng.normal(scale=3.0, size=(15, V)), 8)
+        nodes = T.build_tree(top_idx, top_lp, budget)
+        toks = torch.tensor([[int(rng.integers(0, V))] + [nd.token for nd in nodes]], device=gpu)
+        pos = torch.tensor([[S] + [S + nd.depth for nd in nodes]], device=gpu)
+        mask = tree_attention_mask(S, nodes, gpu, torch.bfloat16)
+        logits = {}
+        for impl in ("sdpa", "cast_tree"):
+            model.config._attn_implementation = impl
+            c = copy.deepcopy(cache)
+            logits[impl] = model(toks, position_ids=pos, past_key_values=c, use_cache=True,
+                                 attention_mask=mask).logits[0].float()
+        model.config._attn_implementation = "sdpa"
+        w, g = logits["sdpa"], logits["cast_tree"]
+        scale = w.abs().max().item()
+        err = (g - w).abs().max().item()
+        print(f"  logits max |diff| {err:.3e} (scale {scale:.2f})", flush=True)
+        assert err <= 2e-2 * scale
+        assert OW.greedy_walk(nodes, g.cpu()) == OW.greedy_walk(nodes, w.cpu())
+    # a forward without a tree mask (prefill) goes through plain SDPA
+    model.config._attn_implementation = "cast_tree"
+    ids = torch.from_numpy(rng.integers(0, V, size=40)).to(gpu)[None]
+    a = model(ids).logits
+    model.config._attn_implementation = "sdpa"
+    b = model(ids).logits
+    assert torch.equal(a, b)
