@@ -198,6 +198,50 @@ def store_layout(dev, steps, warmup):
     return dict(inplace_us=round(t_in, 2), assembled_us=round(t_as, 2), cap=cap)
 
 
+def kv_append(dev, steps, warmup, layers=36):
+    """The accepted-path KV append after a verify round (cast_trees/serving.py:
+    264-289) at Qwen3-8B shapes: 36 layers, B=8, 8 KV heads, D=128, stores of
+    8192 + 320 slots, packs of 128, a planted accepted path per request: one
+    fused launch driven by greedy_accept's device outputs, against the
+    reference's two indexed copies per layer."""
+    import torch
+    from cast_amd import greedy_accept, scenarios, serving
+    wl = scenarios.qwen3_headline()
+    meta = wl.meta_tensors(dev)
+    logits, _ = scenarios.planted_logits(wl, seed=0)
+    path, plen, _, _ = greedy_accept(logits.to(dev), meta["cu_q"], meta["parent"],
+                                     torch.from_numpy(wl.packed.token).to(dev))
+    del logits
+    B, Hkv, D, cap = wl.B, wl.Hkv, wl.D, int(wl.prefix_len[0]) + 320
+    g = torch.Generator(device=dev).manual_seed(3)
+    buf_k = [torch.empty((B, Hkv, cap, D), dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+    buf_v = [torch.empty_like(x) for x in buf_k]
+    pack_k = [torch.randn((Hkv, wl.total_q, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    pack_v = [torch.randn((Hkv, wl.total_q, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    store_len = torch.from_numpy(wl.prefix_len.astype("int32")).to(dev)
+    plen_h, path_h = plen.cpu().tolist(), path.cpu().tolist()
+    src, dst_b, dst_p = [], [], []
+    for b in range(B):
+        for j, pk in enumerate([0] + [i + 1 for i in path_h[b][:plen_h[b]]]):
+            src.append(int(wl.cu_q[b]) + pk)
+            dst_b.append(b)
+            dst_p.append(int(wl.prefix_len[b]) + j)
+    src, dst_b, dst_p = (torch.tensor(x, dtype=torch.long, device=dev) for x in (src, dst_b, dst_p))
+
+    def fused():
+        serving.append_accepted(buf_k, buf_v, store_len, meta["cu_q"], path, plen, pack_k, pack_v)
+
+    def per_layer():
+        for li in range(layers):
+            buf_k[li][dst_b, :, dst_p] = pack_k[li][:, src].permute(1, 0, 2)
+            buf_v[li][dst_b, :, dst_p] = pack_v[li][:, src].permute(1, 0, 2)
+
+    t_f = time_kernel(fused, steps, warmup)
+    t_r = time_kernel(per_layer, steps, warmup)
+    log(f"  kv append ({layers} layers, {len(src)} rows): fused {t_f:.1f} us, per-layer indexing {t_r:.1f} us")
+    return dict(fused_us=round(t_f, 2), per_layer_indexing_us=round(t_r, 2), layers=layers, rows=len(src))
+
+
 def secondary(dev, steps, warmup):
     import torch
     from cast_amd import greedy_accept, scenarios, tree_bitmask
@@ -216,6 +260,7 @@ def secondary(dev, steps, warmup):
         del h
         torch.cuda.empty_cache()
     res["store_layout"] = store_layout(dev, steps, warmup)
+    res["kv_append"] = kv_append(dev, steps, warmup)
     # K1 and K3 on the headline trees, full Qwen3 vocabulary logits
     wl = scenarios.qwen3_headline()
     meta = wl.meta_tensors(dev)

@@ -1,0 +1,127 @@
+// K4: accepted-path KV append into the per-request store, all layers in one
+// launch.
+//
+// Replaces the per-layer scatter of cast_trees/serving.py:264-289
+// (_append_store): for every surviving request b, the pack rows it keeps -
+// the root and its accepted nodes, keep = [0] + [i + 1 for i in path]
+// (serving.py:328-330) - are copied from the verify pass's pack K/V of each
+// layer (serving.py:62, [Hkv, total_q, D]) to store slots
+// store_len[b] .. store_len[b] + len(path) of buf[layer][b] ([B, Hkv, cap, D]).
+// The reference issues two advanced-indexing copies per layer; here one
+// workgroup per (request, layer) moves 16-byte chunks, driven by the
+// greedy-accept kernel's device-side path / path_len (no host round trip).
+#include "cast_common.hpp"
+
+namespace cast {
+
+struct AppendArgs {
+    const void *const *k_pack;   // [layers] pack K of each layer
+    const void *const *v_pack;
+    void *const *k_store;        // [layers] store K of each layer
+    void *const *v_store;
+    int32_t layers, batch, total_q, cap, Hkv, chunks;   // chunks = 16-byte pieces per (row, head)
+    const int32_t *src_row;      // [batch] packed row of request b's root (cu_q of its pack)
+    const int32_t *path;         // [batch][path_stride] accepted node indices (-1 padded)
+    int32_t path_stride;
+    const int32_t *path_len;     // [batch]
+    const int32_t *store_len;    // [batch] tokens already in request b's slot
+    int32_t *new_len;            // [batch] out: store_len + path_len + 1 (nullable)
+    int64_t kp_tok, kp_head, vp_tok, vp_head;             // bytes
+    int64_t ks_batch, ks_head, ks_tok, vs_batch, vs_head, vs_tok;   // bytes
+    int32_t *status;
+};
+
+__global__ __launch_bounds__(256) void store_append_kernel(AppendArgs a) {
+    const int b = blockIdx.x, layer = blockIdx.y;
+    const int n = a.path_len[b];
+    const int s0 = a.store_len[b];
+    const int root = a.src_row[b];
+    const int count = n + 1;     // root + accepted nodes
+    if (n < 0 || n >= kMaxPack || s0 < 0 || s0 + count > a.cap || root < 0 || root >= a.total_q) {
+        if (threadIdx.x == 0 && layer == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        return;
+    }
+    if (threadIdx.x == 0 && layer == 0 && a.new_len) a.new_len[b] = s0 + count;
+    const char *kp = static_cast<const char *>(a.k_pack[layer]);
+    const char *vp = static_cast<const char *>(a.v_pack[layer]);
+    char *ks = static_cast<char *>(a.k_store[layer]) + (int64_t)b * a.ks_batch;
+    char *vs = static_cast<char *>(a.v_store[layer]) + (int64_t)b * a.vs_batch;
+    const int per_row = a.Hkv * a.chunks;
+    for (int idx = threadIdx.x; idx < count * per_row; idx += blockDim.x) {
+        const int j = idx / per_row;
+        const int h = (idx / a.chunks) % a.Hkv;
+        const int c = idx % a.chunks;
+        // keep[j]: the root (pack index 0), then node path[j-1] at pack index path[j-1] + 1
+        int pk = 0;
+        if (j > 0) {
+            const int node = a.path[(int64_t)b * a.path_stride + j - 1];
+            pk = node + 1;
+            if (node < 0 || root + pk >= a.total_q) {
+                raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+                continue;
+            }
+        }
+        const int64_t src = (int64_t)(root + pk);
+        const int64_t dst = (int64_t)(s0 + j);
+        const u32x4 kx = *reinterpret_cast<const u32x4 *>(kp + src * a.kp_tok + h * a.kp_head + c * 16);
+        const u32x4 vx = *reinterpret_cast<const u32x4 *>(vp + src * a.vp_tok + h * a.vp_head + c * 16);
+        *reinterpret_cast<u32x4 *>(ks + h * a.ks_head + dst * a.ks_tok + c * 16) = kx;
+        *reinterpret_cast<u32x4 *>(vs + h * a.vs_head + dst * a.vs_tok + c * 16) = vx;
+    }
+}
+
+}  // namespace cast
+
+using namespace cast;
+
+extern "C" int cast_store_append(const void *const *k_pack, const void *const *v_pack, void *const *k_store,
+                                 void *const *v_store, int32_t layers, const int32_t *src_row,
+                                 const int32_t *path, int32_t path_stride, const int32_t *path_len,
+                                 const int32_t *store_len, int32_t *new_len, int32_t batch, int32_t total_q,
+                                 int32_t cap, int32_t num_kv_heads, int32_t head_dim, int64_t kp_tok,
+                                 int64_t kp_head, int64_t vp_tok, int64_t vp_head, int64_t ks_batch,
+                                 int64_t ks_head, int64_t ks_tok, int64_t vs_batch, int64_t vs_head,
+                                 int64_t vs_tok, int32_t dtype, int32_t *status, cast_stream_t stream) {
+    if (layers < 0 || batch < 0 || total_q < 0 || cap < 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+        path_stride < kMaxPack)
+        return CAST_ERR_SHAPE;
+    if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
+    if (layers == 0 || batch == 0) return CAST_OK;
+    if (!k_pack || !v_pack || !k_store || !v_store || !src_row || !path || !path_len || !store_len)
+        return CAST_ERR_NULL_POINTER;
+    const int64_t esz = dtype == CAST_BF16 ? 2 : 4;
+    if ((head_dim * esz) % 16) return CAST_ERR_HEAD_DIM;
+    const int64_t strides[10] = {kp_tok, kp_head, vp_tok, vp_head, ks_batch, ks_head, ks_tok, vs_batch, vs_head, vs_tok};
+    for (int64_t s : strides)
+        if ((s * esz) % 16) return CAST_ERR_ALIGNMENT;
+    AppendArgs a{};
+    a.k_pack = k_pack;
+    a.v_pack = v_pack;
+    a.k_store = k_store;
+    a.v_store = v_store;
+    a.layers = layers;
+    a.batch = batch;
+    a.total_q = total_q;
+    a.cap = cap;
+    a.Hkv = num_kv_heads;
+    a.chunks = (int32_t)(head_dim * esz / 16);
+    a.src_row = src_row;
+    a.path = path;
+    a.path_stride = path_stride;
+    a.path_len = path_len;
+    a.store_len = store_len;
+    a.new_len = new_len;
+    a.kp_tok = kp_tok * esz;
+    a.kp_head = kp_head * esz;
+    a.vp_tok = vp_tok * esz;
+    a.vp_head = vp_head * esz;
+    a.ks_batch = ks_batch * esz;
+    a.ks_head = ks_head * esz;
+    a.ks_tok = ks_tok * esz;
+    a.vs_batch = vs_batch * esz;
+    a.vs_head = vs_head * esz;
+    a.vs_tok = vs_tok * esz;
+    a.status = status;
+    store_append_kernel<<<dim3(batch, layers), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+    return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
+}

@@ -12,6 +12,10 @@ Mirrors the attention side of cast_trees/serving.py:
   begin_verify        the packing half of BatchedServer._verify_varlen
                       (serving.py:208-253): packed tokens, positions,
                       offsets and ancestor words, then PLAN.set
+  append_store        BatchedServer._append_store (serving.py:264-289): the
+                      accepted rows of every layer into the store in one
+                      launch; append_accepted does it from greedy_accept's
+                      device outputs without a host sync
   _tree_attention     the batch-one verify of cast_trees/decode.py:166-171
                       (target forward with the additive tree mask of
                       cast_trees/verify.py:15-25) through the same kernel,
@@ -148,6 +152,106 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
     ids = torch.tensor([tok], dtype=torch.long, device=dev)
     pos_ids = torch.tensor([pos], dtype=torch.long, device=dev)
     return ids, pos_ids, cu_q
+
+
+# ---- accepted-path KV append (cast_trees/serving.py:264-289)
+
+def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_len, new_len, status=None):
+    """One cast_store_append launch over every layer (all arguments device
+    tensors; buf_* / pack_* lists of per-layer tensors)."""
+    from . import _lib
+    from .tree_attn import _DTYPES
+    lib = _lib.load()
+    L = len(buf_k)
+    if not (len(buf_v) == len(pack_k) == len(pack_v) == L) or L == 0:
+        raise ValueError("one store and one pack K/V tensor per layer")
+    k0, p0 = buf_k[0], pack_k[0]
+    B, Hkv, cap, D = (int(x) for x in k0.shape)
+    total_q = int(p0.shape[1])
+    for t in (*buf_k, *buf_v):
+        if tuple(t.shape) != (B, Hkv, cap, D) or t.stride() != k0.stride() or t.dtype != k0.dtype:
+            raise ValueError("every layer's store must share shape, strides and dtype")
+    for t in (*pack_k, *pack_v):
+        if tuple(t.shape) != (Hkv, total_q, D) or t.stride() != p0.stride() or t.dtype != k0.dtype:
+            raise ValueError(f"pack K/V must be [{Hkv}, total_q, {D}] with the store's dtype, alike in every layer")
+        if t.stride(-1) != 1 or t.data_ptr() % 16:
+            raise ValueError("pack K/V need a contiguous, 16-byte aligned head dim")
+    if k0.stride(-1) != 1 or any(t.data_ptr() % 16 for t in (*buf_k, *buf_v)):
+        raise ValueError("the store needs a contiguous, 16-byte aligned head dim")
+    n = int(src_row.shape[0])
+    if n > B or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
+        raise ValueError("path must be [B, >=128] (as written by greedy_accept) for B <= the store batch")
+    dev = k0.device
+    ptrs = torch.tensor([t.data_ptr() for t in (*pack_k, *pack_v, *buf_k, *buf_v)], dtype=torch.int64, device=dev)
+    pk, pv, sk, sv = (ptrs[i * L:(i + 1) * L] for i in range(4))
+    with torch.cuda.device(dev):
+        st = lib.cast_store_append(
+            _lib.ptr(pk), _lib.ptr(pv), _lib.ptr(sk), _lib.ptr(sv), L, _lib.ptr(src_row), _lib.ptr(path),
+            path.stride(0), _lib.ptr(path_len), _lib.ptr(store_len), _lib.ptr(new_len), n, total_q, cap, Hkv, D,
+            p0.stride(1), p0.stride(0), pack_v[0].stride(1), pack_v[0].stride(0), k0.stride(0), k0.stride(1),
+            k0.stride(2), buf_v[0].stride(0), buf_v[0].stride(1), buf_v[0].stride(2), _DTYPES[k0.dtype],
+            _lib.ptr(status), _lib.stream_of(k0))
+    _lib.check(st, "cast_store_append")
+
+
+def append_accepted(buf_k, buf_v, store_len, cu_q, path, path_len, pack_k=None, pack_v=None, *, check=False):
+    """Append every request's root and accepted nodes to its store slot, all
+    layers in one launch, straight from greedy_accept's device outputs.
+
+    store_len, cu_q: int32 device tensors [B] / [B+1]; path int32 [B, 128],
+    path_len int32 [B] (greedy_accept).  pack_k / pack_v default to PACK_KV.
+    Returns the new lengths (int32 [B], on the device).  No host sync.
+    """
+    pack_k = PACK_KV["k"] if pack_k is None else pack_k
+    pack_v = PACK_KV["v"] if pack_v is None else pack_v
+    dev = buf_k[0].device
+    store_len = torch.as_tensor(store_len, device=dev).to(torch.int32).contiguous()
+    cu_q = torch.as_tensor(cu_q, device=dev).to(torch.int32).contiguous()
+    new_len = torch.empty_like(store_len)
+    status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
+    _append_launch(buf_k, buf_v, pack_k, pack_v, cu_q[:-1].contiguous(), path.to(torch.int32),
+                   path_len.to(torch.int32).contiguous(), store_len, new_len, status)
+    if check:
+        from . import _lib
+        _lib.raise_device_flags(status.item(), "append_accepted")
+    return new_len
+
+
+def append_store(buf_k, buf_v, store_len, cu_q, keep, accepted, rows):
+    """Drop-in for BatchedServer._append_store (cast_trees/serving.py:264-289).
+
+    Keeps the surviving requests ``rows`` (compacting the stores when some
+    finished, growing them when a slot would overflow, as the reference does)
+    and appends request b's packed rows cu_q[b] + keep[b][j] (keep[b] = [0] +
+    [i + 1 for i in path]) at slots store_len[b] + j.  The scatter over every
+    layer is one kernel launch.  Returns (buf_k, buf_v, new_len).
+    """
+    dev = buf_k[0].device
+    if len(rows) != len(store_len):
+        idx = torch.tensor(rows, dtype=torch.long, device=dev)
+        buf_k = [x[idx] for x in buf_k]
+        buf_v = [x[idx] for x in buf_v]
+    new_len = [int(store_len[b]) + int(accepted[b]) for b in rows]
+    cap = int(buf_k[0].shape[2])
+    if new_len and max(new_len) > cap:
+        new_cap = max(max(new_len), 2 * cap)
+        grow = lambda x: torch.cat([x, x.new_zeros(x.shape[0], x.shape[1], new_cap - cap, x.shape[3])], 2)
+        buf_k, buf_v = [grow(x) for x in buf_k], [grow(x) for x in buf_v]
+    if not rows:
+        return buf_k, buf_v, new_len
+    path = np.full((len(rows), MAX_PACK), -1, dtype=np.int32)
+    meta = np.zeros((3, len(rows)), dtype=np.int32)
+    for nb, b in enumerate(rows):
+        kb = list(keep[b])
+        if not kb or kb[0] != 0 or len(kb) != int(accepted[b]) or len(kb) > MAX_PACK:
+            raise ValueError("keep[b] must be [0] + [i + 1 for i in path] with accepted[b] entries")
+        path[nb, :len(kb) - 1] = [k - 1 for k in kb[1:]]
+        meta[:, nb] = (int(cu_q[b]), len(kb) - 1, int(store_len[b]))
+    host = torch.from_numpy(np.concatenate([meta.ravel(), path.ravel()])).to(dev)
+    n = len(rows)
+    _append_launch(buf_k, buf_v, PACK_KV["k"], PACK_KV["v"], host[:n], host[3 * n:].view(n, MAX_PACK),
+                   host[n:2 * n], host[2 * n:3 * n], None)
+    return buf_k, buf_v, new_len
 
 
 # ---- batch-one verify (cast_trees/decode.py:166-171): the target forward over

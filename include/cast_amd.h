@@ -196,6 +196,34 @@ int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t vocab, int
                        int32_t *path_len, int64_t *bonus, int32_t *status,
                        cast_stream_t stream);
 
+/* ---------------------------------------------------------------------
+ * K4: accepted-path KV append into the per-request store, every layer in
+ * one launch.  Replaces the per-layer scatter of cast_trees/serving.py:
+ * 264-289 (_append_store, two indexed copies per layer).
+ *   k_pack / v_pack    device arrays of `layers` pointers to each layer's
+ *                      pack K / V [Hkv, total_q, D] (strides kp_* / vp_*,
+ *                      in elements, shared by all layers)
+ *   k_store / v_store  device arrays of `layers` pointers to each layer's
+ *                      store [batch, Hkv, cap, D] (strides ks_* / vs_*)
+ *   src_row   int32 [batch]  packed row of request b's root (cu_q of its pack)
+ *   path      int32 [batch][path_stride >= 128]  accepted node indices, as
+ *             written by cast_greedy_accept;  path_len int32 [batch]
+ *   store_len int32 [batch]  tokens already in request b's slot
+ *   new_len   int32 [batch]  out (nullable): store_len + path_len + 1
+ * Request b keeps its root and its accepted nodes (keep = [0] + [i + 1 for
+ * i in path], cast_trees/serving.py:328-330) at slots store_len[b] .. in
+ * order.  A request that would pass `cap` is skipped and flagged
+ * CAST_FLAG_BAD_OFFSETS.
+ * ------------------------------------------------------------------- */
+int cast_store_append(const void *const *k_pack, const void *const *v_pack, void *const *k_store,
+                      void *const *v_store, int32_t layers, const int32_t *src_row,
+                      const int32_t *path, int32_t path_stride, const int32_t *path_len,
+                      const int32_t *store_len, int32_t *new_len, int32_t batch, int32_t total_q,
+                      int32_t cap, int32_t num_kv_heads, int32_t head_dim, int64_t kp_tok,
+                      int64_t kp_head, int64_t vp_tok, int64_t vp_head, int64_t ks_batch,
+                      int64_t ks_head, int64_t ks_tok, int64_t vs_batch, int64_t vs_head,
+                      int64_t vs_tok, int32_t dtype, int32_t *status, cast_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

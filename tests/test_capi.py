@@ -106,3 +106,13 @@ def test_store_attention_host_validation(lib):
     assert _store(lib, dtype=2) == 4
     assert _store(lib, scale=-1.0) == 9
     assert _store(lib, B=0) == 0                         # nothing to do
+
+
+def test_store_append_host_validation(lib):
+    f = lib.cast_store_append
+    args = lambda **o: [o.get("ptr", None)] * 4 + [o.get("layers", 2)] + [None] * 2 + [o.get("stride", 128)] + \
+        [None] * 3 + [o.get("B", 2), 16, 64, 4, 128] + [8] * 10 + [o.get("dtype", 0), None, None]
+    assert f(*args()) == 1                       # null pointers
+    assert f(*args(stride=64)) == 7              # path rows narrower than 128
+    assert f(*args(dtype=3)) == 4                # dtype
+    assert f(*args(B=0)) == 0 and f(*args(layers=0)) == 0

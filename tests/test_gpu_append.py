@@ -1,0 +1,124 @@
+"""Accepted-path KV append (cast_trees/serving.py:264-289) on the GPU.
+
+Bar: bit-identical stores and lengths against a torch restatement of the
+reference's _append_store (batch compaction, capacity growth, then per layer
+buf[dst_b, :, dst_p] = pack[:, src].permute(1, 0, 2)).
+"""
+import numpy as np
+import pytest
+import torch
+
+from cast_amd import scenarios as SC
+
+pytestmark = pytest.mark.gpu
+
+
+def _reference_append(buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted, rows):
+    dev = buf_k[0].device
+    src, dst_b, dst_p, new_len = [], [], [], []
+    for nb, b in enumerate(rows):
+        for j, pk in enumerate(keep[b]):
+            src.append(cu_q[b] + pk)
+            dst_b.append(nb)
+            dst_p.append(store_len[b] + j)
+        new_len.append(store_len[b] + accepted[b])
+    if len(rows) != len(store_len):
+        idx = torch.tensor(rows, dtype=torch.long, device=dev)
+        buf_k = [x[idx] for x in buf_k]
+        buf_v = [x[idx] for x in buf_v]
+    cap = buf_k[0].shape[2]
+    if max(new_len) > cap:
+        new_cap = max(max(new_len), 2 * cap)
+        grow = lambda x: torch.cat([x, x.new_zeros(x.shape[0], x.shape[1], new_cap - cap, x.shape[3])], 2)
+        buf_k, buf_v = [grow(x) for x in buf_k], [grow(x) for x in buf_v]
+    src = torch.tensor(src, dtype=torch.long, device=dev)
+    dst_b = torch.tensor(dst_b, dtype=torch.long, device=dev)
+    dst_p = torch.tensor(dst_p, dtype=torch.long, device=dev)
+    for li in range(len(buf_k)):
+        buf_k[li][dst_b, :, dst_p] = pack_k[li][:, src].permute(1, 0, 2)
+        buf_v[li][dst_b, :, dst_p] = pack_v[li][:, src].permute(1, 0, 2)
+    return buf_k, buf_v, new_len
+
+
+def _setup(dev, seed, B=5, L=3, Hkv=4, D=128, cap=96, dtype=torch.bfloat16):
+    rng = np.random.default_rng(seed)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pack_len = [int(x) for x in rng.integers(1, 40, size=B)]
+    cu_q = [0] + list(np.cumsum(pack_len))
+    total_q = cu_q[-1]
+    store_len = [int(x) for x in rng.integers(0, cap - 20, size=B)]
+    buf_k = [torch.randn((B, Hkv, cap, D), generator=g, device=dev).to(dtype) for _ in range(L)]
+    buf_v = [torch.randn((B, Hkv, cap, D), generator=g, device=dev).to(dtype) for _ in range(L)]
+    # HF hands the pack over as key[0]: [Hkv, total_q, D] viewed from token-major storage
+    pack_k = [torch.randn((total_q, Hkv, D), generator=g, device=dev).to(dtype).transpose(0, 1) for _ in range(L)]
+    pack_v = [torch.randn((total_q, Hkv, D), generator=g, device=dev).to(dtype).transpose(0, 1) for _ in range(L)]
+    keep, accepted = [], []
+    for b in range(B):
+        n = int(rng.integers(0, min(pack_len[b], 12)))
+        path = sorted(rng.choice(np.arange(pack_len[b] - 1), size=min(n, pack_len[b] - 1), replace=False).tolist())
+        keep.append([0] + [i + 1 for i in path])
+        accepted.append(len(path) + 1)
+    return buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted
+
+
+@pytest.mark.parametrize("case", ["all-rows", "compact", "grow", "fp32-d64"])
+def test_append_store_matches_reference(gpu, case):
+    from cast_amd import serving
+    kw = dict(D=64, dtype=torch.float32) if case == "fp32-d64" else {}
+    buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=len(case), **kw)
+    B = len(store_len)
+    rows = [0, 2, 3] if case == "compact" else list(range(B))
+    if case == "grow":
+        store_len[1] = buf_k[0].shape[2] - 1          # one slot left: the append must grow the stores
+        keep[1], accepted[1] = [0, 1, 2], 3
+    print(f"case append-{case}: B={B} rows={rows} store_len={store_len} accepted={accepted}", flush=True)
+    ref = _reference_append([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
+                            cu_q, keep, accepted, rows)
+    serving.PACK_KV["k"], serving.PACK_KV["v"] = pack_k, pack_v
+    got = serving.append_store([x.clone() for x in buf_k], [x.clone() for x in buf_v], store_len, cu_q, keep,
+                               accepted, rows)
+    torch.cuda.synchronize()
+    assert got[2] == ref[2]
+    for a, b in zip(got[0] + got[1], ref[0] + ref[1]):
+        assert a.shape == b.shape and torch.equal(a, b)
+
+
+def test_append_accepted_from_greedy_accept(gpu):
+    # the device path: greedy_accept's path / path_len drive the append, no host sync
+    from cast_amd import greedy_accept, serving
+    wl = SC.qwen3_ragged(seed=3, B=4, lo=64, hi=200, packs=(16, 64, 128), vocab=4096)
+    logits, _ = SC.planted_logits(wl, seed=1)
+    meta = wl.meta_tensors(gpu)
+    path, plen, bonus, _ = greedy_accept(logits.to(gpu), meta["cu_q"], meta["parent"],
+                                         torch.from_numpy(wl.packed.token).to(gpu))
+    L, Hkv, D, cap = 2, wl.Hkv, wl.D, 400
+    g = torch.Generator(device=gpu).manual_seed(0)
+    store_len = [int(x) for x in wl.prefix_len]
+    buf_k = [torch.randn((wl.B, Hkv, cap, D), generator=g, device=gpu).to(torch.bfloat16) for _ in range(L)]
+    buf_v = [torch.randn((wl.B, Hkv, cap, D), generator=g, device=gpu).to(torch.bfloat16) for _ in range(L)]
+    pack_k = [torch.randn((Hkv, wl.total_q, D), generator=g, device=gpu).to(torch.bfloat16) for _ in range(L)]
+    pack_v = [torch.randn((Hkv, wl.total_q, D), generator=g, device=gpu).to(torch.bfloat16) for _ in range(L)]
+    print(f"case append-accepted: B={wl.B} store_len={store_len}", flush=True)
+    got_k, got_v = [x.clone() for x in buf_k], [x.clone() for x in buf_v]
+    new_len = serving.append_accepted(got_k, got_v, store_len, meta["cu_q"], path, plen, pack_k, pack_v, check=True)
+    plen_h, path_h = plen.cpu().tolist(), path.cpu().tolist()
+    keep = [[0] + [i + 1 for i in path_h[b][:plen_h[b]]] for b in range(wl.B)]
+    accepted = [len(k) for k in keep]
+    ref = _reference_append([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
+                            [int(x) for x in wl.cu_q], keep, accepted, list(range(wl.B)))
+    assert new_len.cpu().tolist() == ref[2]
+    assert max(accepted) > 1
+    for a, b in zip(got_k + got_v, ref[0] + ref[1]):
+        assert torch.equal(a, b)
+
+
+def test_append_overflow_is_flagged(gpu):
+    from cast_amd import serving
+    buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=9, B=2)
+    cap = buf_k[0].shape[2]
+    path = torch.full((2, 128), -1, dtype=torch.int32, device=gpu)
+    path[:, 0] = 0
+    plen = torch.tensor([1, 1], dtype=torch.int32, device=gpu)
+    print("case append-overflow", flush=True)
+    with pytest.raises(ValueError, match="inconsistent"):
+        serving.append_accepted(buf_k, buf_v, [cap - 1, 0], cu_q, path, plen, pack_k, pack_v, check=True)
