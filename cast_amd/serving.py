@@ -156,6 +156,22 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
 
 # ---- accepted-path KV append (cast_trees/serving.py:264-289)
 
+_PTR_TABLES = {}    # (device, addresses) -> device int64 table, reused while the buffers stay put
+
+
+def _pointer_table(dev, addrs):
+    """Device array of per-layer base addresses.  Built (one host-to-device
+    copy) only when the addresses change, i.e. after the stores or the pack
+    buffers were reallocated."""
+    key = (str(dev), tuple(addrs))
+    t = _PTR_TABLES.get(key)
+    if t is None:
+        if len(_PTR_TABLES) > 8:
+            _PTR_TABLES.clear()
+        t = _PTR_TABLES[key] = torch.tensor(addrs, dtype=torch.int64, device=dev)
+    return t
+
+
 def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_len, new_len, status=None):
     """One cast_store_append launch over every layer (all arguments device
     tensors; buf_* / pack_* lists of per-layer tensors)."""
@@ -182,7 +198,7 @@ def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_
     if n > B or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
         raise ValueError("path must be [B, >=128] (as written by greedy_accept) for B <= the store batch")
     dev = k0.device
-    ptrs = torch.tensor([t.data_ptr() for t in (*pack_k, *pack_v, *buf_k, *buf_v)], dtype=torch.int64, device=dev)
+    ptrs = _pointer_table(dev, [t.data_ptr() for t in (*pack_k, *pack_v, *buf_k, *buf_v)])
     pk, pv, sk, sv = (ptrs[i * L:(i + 1) * L] for i in range(4))
     with torch.cuda.device(dev):
         st = lib.cast_store_append(
