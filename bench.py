@@ -242,6 +242,37 @@ def kv_append(dev, steps, warmup, layers=36):
     return dict(fused_us=round(t_f, 2), per_layer_indexing_us=round(t_r, 2), layers=layers, rows=len(src))
 
 
+def draft_trees(dev, steps, warmup):
+    """Drafting at Qwen3-8B shapes: B=8 requests x 15 future positions x the
+    151936-entry vocabulary (bf16 logits), top-8 per position, one best-first
+    tree of 127 nodes per request.  The device path (cast_draft_topk +
+    cast_build_trees) against the reference flow: torch log_softmax + topk on
+    the GPU, a copy to the host, and the heap of cast_trees/tree.py:29-49."""
+    import numpy as np
+    import torch
+    from cast_amd import tree as T
+    from cast_amd.draft import build_trees, topk_marginals
+    B, L, V = 8, 15, 151936
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = (torch.randn((B * L, V), generator=g, device=dev) * 4).to(torch.bfloat16)
+    bud = torch.full((B,), 127, dtype=torch.int32, device=dev)
+
+    def device():
+        idx, lp = topk_marginals(x, 8, on_device=True)
+        build_trees(idx.view(B, L, 8), lp.view(B, L, 8), bud)
+
+    def reference_flow():
+        top = torch.topk(torch.nn.functional.log_softmax(x.float(), dim=-1), 8, dim=-1)
+        ti, tl = top.indices.cpu().numpy(), top.values.cpu().numpy()
+        for b in range(B):
+            T.build_tree(ti[b * L:(b + 1) * L], tl[b * L:(b + 1) * L], 127)
+
+    t_d = time_kernel(device, steps, warmup)
+    t_r = time_kernel(reference_flow, max(3, steps // 5), 2)
+    log(f"  draft trees (B={B}, 127 nodes): device {t_d:.1f} us, torch topk + host heap {t_r:.1f} us")
+    return dict(device_us=round(t_d, 2), torch_topk_host_heap_us=round(t_r, 2), batch=B, nodes=127)
+
+
 def secondary(dev, steps, warmup):
     import torch
     from cast_amd import greedy_accept, scenarios, tree_bitmask
@@ -261,6 +292,7 @@ def secondary(dev, steps, warmup):
         torch.cuda.empty_cache()
     res["store_layout"] = store_layout(dev, steps, warmup)
     res["kv_append"] = kv_append(dev, steps, warmup)
+    res["draft_trees"] = draft_trees(dev, steps, warmup)
     # K1 and K3 on the headline trees, full Qwen3 vocabulary logits
     wl = scenarios.qwen3_headline()
     meta = wl.meta_tensors(dev)

@@ -25,6 +25,9 @@ _LAZY = {
     "walk_tree": "verify",
     "walk_trees": "verify",
     "tree_attention_mask": "verify",
+    "topk_marginals": "draft",
+    "build_trees": "draft",
+    "build_tree_device": "draft",
 }
 
 __all__ = ["__version__", "MAX_PACK", "PackedTrees", "TreeNode", "ancestor_matrix", "block_topk",

@@ -21,7 +21,7 @@ FLAG_BAD_OFFSETS = 2
 FLAG_BAD_PARENT = 4
 FLAG_TOO_LONG = 8
 
-BF16, FP32 = 0, 1
+BF16, FP32, FP64 = 0, 1, 2
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -44,6 +44,8 @@ SIGNATURES = {
     "cast_tree_attn_default_split": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32], _I32),
     "cast_store_append": ([_P] * 4 + [_I32] + [_P] * 2 + [_I32] + [_P] * 3 + [_I32] * 5 + [_I64] * 10 +
                           [_I32, _P, _P], ctypes.c_int),
+    "cast_draft_topk": ([_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
+    "cast_build_trees": ([_P, _P, _I32, _I32, _I32, _I32] + [_P] * 8, ctypes.c_int),
     "cast_greedy_accept": ([_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P], ctypes.c_int),
 }
 

@@ -52,7 +52,7 @@ enum cast_device_flag {
                                       rows and 2^31 bytes per source) */
 };
 
-enum cast_dtype { CAST_BF16 = 0, CAST_FP32 = 1 };
+enum cast_dtype { CAST_BF16 = 0, CAST_FP32 = 1, CAST_FP64 = 2 };
 
 /* Library ABI version (bumped on any signature change). */
 int cast_abi_version(void);
@@ -223,6 +223,31 @@ int cast_store_append(const void *const *k_pack, const void *const *v_pack, void
                       int64_t kp_head, int64_t vp_tok, int64_t vp_head, int64_t ks_batch,
                       int64_t ks_head, int64_t ks_tok, int64_t vs_batch, int64_t vs_head,
                       int64_t vs_tok, int32_t dtype, int32_t *status, cast_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * K5: drafter top-k marginals and best-first tree build on the device.
+ * cast_draft_topk replaces topk_marginals (cast_trees/verify.py:8-12; the
+ * log_softmax + topk + .cpu() of cast_trees/serving.py:126-128):
+ *   logits   [rows, vocab] bf16 / fp32, row stride logits_ld elements
+ *   top_idx  int64 [rows][k] token ids, top_lp  float [rows][k] log-probs,
+ *            ranked by descending log-probability, equal values in
+ *            increasing index order (cast_trees/tree.py:20-26); 1 <= k <= 16;
+ *            finite logits
+ * cast_build_trees replaces build_tree (cast_trees/tree.py:29-49), one tree
+ * per request, the same heap order (-score, depth, parent, rank, counter):
+ *   top_idx / top_lp  [batch][L][k] as written by cast_draft_topk; top_lp
+ *            float (lp_dtype CAST_FP32) or double (CAST_FP64)
+ *   budget   int32 [batch] non-root nodes wanted (<= 127)
+ *   token int64, depth int32, parent int32 (node index, -1 = root child),
+ *   score double: [batch][127] nodes in pop order;  n_nodes int32 [batch]
+ * ------------------------------------------------------------------- */
+int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t rows, int32_t vocab,
+                    int32_t dtype, int32_t k, int64_t *top_idx, float *top_lp,
+                    cast_stream_t stream);
+int cast_build_trees(const int64_t *top_idx, const void *top_lp, int32_t lp_dtype, int32_t batch,
+                     int32_t L, int32_t k, const int32_t *budget, int64_t *token, int32_t *depth,
+                     int32_t *parent, double *score, int32_t *n_nodes, int32_t *status,
+                     cast_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,8 @@ Contents, each restating the reference algorithm it cites:
                62,73-75,89, cast_trees/verify.py:15-25)
   walk.py      greedy accepted-path walk
                (cast_trees/decode.py:13-17, 85-103)
+  draft.py     drafter top-k over the log-softmax and the best-first tree
+               build (cast_trees/tree.py:20-49, cast_trees/verify.py:8-12)
 
 Pinning (what fixes each function independently of its own formula):
   bitmask  - reference int64 recurrence of serving.py:218-222 (a different
@@ -22,6 +24,10 @@ Pinning (what fixes each function independently of its own formula):
   attn     - P=1 and chain trees reduce to torch SDPA (decode / causal);
              S=0 star trees reduce to per-row closed forms; masked keys with
              poisoned values must not leak; LSE matches torch.logsumexp.
+  draft    - the reference module's own outputs on seeded inputs
+             (tests/golden/tree_fixtures.json: top-k ids and log-probs,
+             trees of 15..127 nodes), exact; prefix-closure and descending
+             scores along every root path.
   walk     - replay-style accepted length (cast_trees/replay.py:20-32, a
              rank-tuple path-set formulation), planted-path workloads, and
              brute force over every root path on tiny trees.

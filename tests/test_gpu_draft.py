@@ -1,0 +1,88 @@
+"""Drafter top-k and best-first tree build on the GPU.
+
+Bars: top-k token ids identical to the oracle (descending log-probability,
+equal values by increasing index), log-probs within 2e-5; trees identical
+node for node (token, depth, parent, and the double-precision score) to the
+reference module's own trees (tests/golden/tree_fixtures.json) from the same
+float64 log-probs, and to the oracle's heap from float32 log-probs.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import draft as OD
+
+pytestmark = pytest.mark.gpu
+
+FIX = json.loads((Path(__file__).parent / "golden" / "tree_fixtures.json").read_text())
+
+
+@pytest.mark.parametrize("dtype,k", [(torch.float32, 8), (torch.bfloat16, 8), (torch.float32, 16)])
+def test_topk_marginals_match_oracle(gpu, dtype, k):
+    from cast_amd.draft import topk_marginals
+    rng = np.random.default_rng(k)
+    x = rng.normal(scale=5.0, size=(15, 151936)).astype(np.float32)
+    x[3, [10, 99, 151935]] = x[3].max() + 2.0          # ties at the top of one row
+    xd = torch.from_numpy(x).to(gpu).to(dtype)
+    print(f"case topk {dtype} k={k}", flush=True)
+    idx, lp = topk_marginals(xd, k, on_device=True)
+    torch.cuda.synchronize()
+    want_i, want_lp = OD.topk_log_softmax(xd.float().cpu().numpy(), k)
+    assert idx.cpu().numpy().tolist() == want_i.tolist()
+    assert np.abs(lp.cpu().numpy() - want_lp).max() <= 2e-5
+    if dtype == torch.float32:
+        assert idx[3, :3].cpu().tolist() == [10, 99, 151935]
+    # the drop-in returns host tensors like the reference
+    hi, hl = topk_marginals(xd, k)
+    assert hi.device.type == "cpu" and torch.equal(hi, idx.cpu())
+
+
+def test_build_trees_match_reference_fixtures(gpu):
+    from cast_amd.draft import build_trees
+    cases = [c for c in FIX["cases"] if "127" in c["trees"]]
+    budgets = [int(n) for n in ("15", "31", "63", "127")]
+    print(f"case build-trees: {len(cases)} fixture blocks x budgets {budgets}", flush=True)
+    ti = torch.tensor([c["top_idx"] for c in cases for _ in budgets], dtype=torch.int64, device=gpu)
+    tl = torch.tensor([c["top_lp"] for c in cases for _ in budgets], dtype=torch.float64, device=gpu)
+    bud = torch.tensor([n for _ in cases for n in budgets], dtype=torch.int32, device=gpu)
+    token, depth, parent, score, n_nodes = build_trees(ti, tl, bud, check=True)
+    token, depth, parent, score, n_nodes = (t.cpu() for t in (token, depth, parent, score, n_nodes))
+    row = 0
+    checked = 0
+    for c in cases:
+        for n in budgets:
+            want = c["trees"].get(str(n))
+            m = int(n_nodes[row])
+            if want is not None:
+                got = [[int(token[row, i]), int(depth[row, i]), int(parent[row, i]), float(score[row, i])]
+                       for i in range(m)]
+                assert got == want, f"{c['name']} budget {n}"
+                checked += 1
+            row += 1
+    assert checked >= 20
+
+
+def test_device_draft_pipeline_matches_oracle_heap(gpu):
+    # topk on the device, then the tree on the device, vs the oracle's heap on
+    # the same float32 log-probs; and the TreeNode drop-in
+    from cast_amd.draft import build_tree_device, build_trees, topk_marginals
+    rng = np.random.default_rng(3)
+    B, L, V = 6, 15, 151936
+    x = torch.from_numpy(rng.normal(scale=4.0, size=(B * L, V)).astype(np.float32)).to(gpu).to(torch.bfloat16)
+    print(f"case draft-pipeline B={B}", flush=True)
+    idx, lp = topk_marginals(x, 8, on_device=True)
+    budgets = [15, 48, 127, 1, 63, 100]
+    token, depth, parent, score, n_nodes = build_trees(idx.view(B, L, 8), lp.view(B, L, 8),
+                                                       torch.tensor(budgets, device=gpu))
+    idx_h, lp_h = idx.cpu().numpy().reshape(B, L, 8), lp.cpu().numpy().reshape(B, L, 8)
+    for b in range(B):
+        want = OD.build_tree(idx_h[b], lp_h[b], budgets[b])
+        m = int(n_nodes[b])
+        got = list(zip(token[b, :m].tolist(), depth[b, :m].tolist(), parent[b, :m].tolist(),
+                       score[b, :m].tolist()))
+        assert got == [(t, d, p, s) for t, d, p, s in want]
+    nodes = build_tree_device(idx_h[2], lp_h[2], 127)
+    assert [(n.token, n.depth, n.parent, n.score) for n in nodes] == OD.build_tree(idx_h[2], lp_h[2], 127)

@@ -280,3 +280,49 @@ def test_planted_walk_mistake_is_caught(monkeypatch):
     swapped = [kids_rev[1], kids_rev[0], T.TreeNode(4, 2, 0, 0.0)]
     lg = logits[[0, 2, 1, 3]]
     assert OW.greedy_walk(swapped, lg) != ([0], 5)
+
+
+# ---------------------------------------------------------------- draft
+
+def _fixture_scores(case):
+    name = case["name"]
+    if name == "quickstart-seed0":
+        return np.random.default_rng(0).normal(scale=5, size=(15, 64))
+    if name.startswith("scaled3-seed"):
+        return np.random.default_rng(int(name[-1])).normal(size=(15, 100)) * 3
+    seed = int(name.split("seed")[1].split("-")[0])
+    scale = float(name.split("scale")[1])
+    return np.random.default_rng(seed).normal(scale=scale, size=(15, 151936))
+
+
+def test_draft_oracle_matches_reference_fixtures():
+    # top-k ids and log-probs, and every tree, as the reference module wrote them
+    import json
+    from pathlib import Path
+    from oracle import draft as OD
+    fix = json.loads((Path(__file__).parent / "golden" / "tree_fixtures.json").read_text())
+    for case in fix["cases"]:
+        idx, lp = OD.topk_log_softmax(_fixture_scores(case), case["k"])
+        assert idx.tolist() == case["top_idx"]
+        assert np.array_equal(lp, np.asarray(case["top_lp"]))
+        for n, want in case["trees"].items():
+            got = OD.build_tree(idx, lp, int(n), case["k"])
+            assert [list(g[:3]) for g in got] == [w[:3] for w in want]
+            assert [g[3] for g in got] == [w[3] for w in want]
+
+
+def test_draft_oracle_tree_invariants_and_ties():
+    from oracle import draft as OD
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(15, 300)).astype(np.float32)
+    x[:, 7] = x[:, 11] = x[:, 200] = x.max(axis=1) + 1.0           # a three-way tie at the top
+    idx, lp = OD.topk_log_softmax(x, 8)
+    assert (idx[:, :3] == [7, 11, 200]).all()                       # equal values: increasing index
+    assert (np.diff(lp, axis=1) <= 0).all()
+    nodes = OD.build_tree(idx, lp, 127)
+    assert len(nodes) == 127
+    for i, (_, d, p, s) in enumerate(nodes):
+        assert p < i and (p == -1) == (d == 1)                       # parents first, prefix-closed
+        if p >= 0:
+            assert nodes[p][1] == d - 1 and nodes[p][3] >= s         # a child never outscores its parent
+    assert [n[3] for n in nodes] == sorted([n[3] for n in nodes], reverse=True)   # best-first pop order
