@@ -34,30 +34,41 @@ __device__ __forceinline__ float logit_at(const char *row, int i) {
 }
 
 // One workgroup per row: top-k (value, index) and the row's log-sum-exp.
-// Every thread keeps its best kTopKMax elements (a superset of its share of
-// the row's top k) in a fully unrolled sorted list; k merge rounds then pick
-// the row's top k.
-template <bool BF16>
-__global__ __launch_bounds__(256) void draft_topk_kernel(const void *__restrict__ logits, int64_t ld, int32_t vocab,
+//
+// Each thread keeps its best K elements (K >= k) in a fully unrolled sorted
+// list; k merge rounds of the list heads give the row's top k.  After the
+// first batch (4 chunks of 16 bytes per thread) one merge finds the top k so
+// far; its k-th entry is a threshold no final top-k element ranks after, so
+// later elements that do not rank before it skip the list (the filter is
+// exact), and the merged entries are dealt back one per thread.
+//
+// Log-sum-exp: per 16-byte chunk, the chunk's max updates the thread's
+// running max, the chunk's exp terms are summed in float and the thread's
+// total is rescaled and accumulated in double.
+template <bool BF16, int K>
+__global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict__ logits, int64_t ld, int32_t vocab,
                                                          int32_t k, int64_t *__restrict__ top_idx,
                                                          float *__restrict__ top_lp) {
-    constexpr int NT = 256, K = kTopKMax;
+    constexpr int NT = 512, NW = NT / 64;
+    constexpr float kLog2e = 1.4426950408889634f;
     const int row = blockIdx.x, tid = threadIdx.x;
     const char *base = static_cast<const char *>(logits) + (size_t)row * (size_t)ld * (BF16 ? 2 : 4);
     float tv[K];
     int ti[K];
+    auto clear_list = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-        tv[j] = -INFINITY;
-        ti[j] = INT_MAX;   // empty slot
-    }
-    // pass 1: row maximum and the thread's sorted top-K.  Elements come in
-    // increasing index order, so a new one goes behind equal values.
-    float mx = -INFINITY;
-    for (int i = tid; i < vocab; i += NT) {
-        const float v = logit_at<BF16>(base, i);
-        mx = fmaxf(mx, v);
-        if (v > tv[K - 1] || ti[K - 1] == INT_MAX) {
+        for (int j = 0; j < K; ++j) {
+            tv[j] = -INFINITY;
+            ti[j] = INT_MAX;   // empty slot
+        }
+    };
+    clear_list();
+    float thr_v = -INFINITY;   // elements must rank before (thr_v, thr_i)
+    int thr_i = INT_MAX;
+    // a thread's elements come in increasing index order, so a new element
+    // goes behind equal values already in its list
+    auto consider = [&](float v, int i) __attribute__((always_inline)) {
+        if ((v > tv[K - 1] || ti[K - 1] == INT_MAX) && ranks_before(v, i, thr_v, thr_i)) {
             bool placed = false;
 #pragma unroll
             for (int j = K - 1; j >= 0; --j) {
@@ -74,89 +85,239 @@ __global__ __launch_bounds__(256) void draft_topk_kernel(const void *__restrict_
                 }
             }
         }
-    }
-    __shared__ float red[NT / 64];
-    __shared__ double dred[NT / 64];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = red[0];
-#pragma unroll
-    for (int w = 1; w < NT / 64; ++w) mx = fmaxf(mx, red[w]);
-    // pass 2: sum of exp(x - max), accumulated in double
+    };
+    float mx = -INFINITY;   // running max; sum holds sum(exp(x - mx))
     double sum = 0.0;
-    for (int i = tid; i < vocab; i += NT) sum += (double)expf(logit_at<BF16>(base, i) - mx);
+    auto lse_add = [&](const auto &v) __attribute__((always_inline)) {
+        constexpr int n = sizeof(v) / sizeof(float);
+        float m = v[0];
+#pragma unroll
+        for (int e = 1; e < n; ++e) m = fmaxf(m, v[e]);
+        const float nm = fmaxf(mx, m);
+        const float ref = nm == -INFINITY ? 0.f : nm;
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < n; ++e) part += __builtin_amdgcn_exp2f((v[e] - ref) * kLog2e);
+        sum = sum * (double)__builtin_amdgcn_exp2f((mx - ref) * kLog2e) + (double)part;
+        mx = nm;
+    };
+    // k rounds over the list heads; the row's top k so far, in order, into topv/topi
+    __shared__ float hv[NW], topv[K];
+    __shared__ int hi[NW], topi[K];
+    auto merge = [&]() __attribute__((always_inline)) {
+        for (int r = 0; r < k; ++r) {
+            float bv = tv[0];
+            int bi = ti[0];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(bv, off);
+                const int oi = __shfl_xor(bi, off);
+                if (ranks_before(ov, oi, bv, bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            __syncthreads();
+            if ((tid & 63) == 0) {
+                hv[tid >> 6] = bv;
+                hi[tid >> 6] = bi;
+            }
+            __syncthreads();
+            bv = hv[0];
+            bi = hi[0];
+#pragma unroll
+            for (int w = 1; w < NW; ++w)
+                if (ranks_before(hv[w], hi[w], bv, bi)) {
+                    bv = hv[w];
+                    bi = hi[w];
+                }
+            if (ti[0] == bi && bi != INT_MAX) {   // indices are disjoint across threads: one owner pops
+#pragma unroll
+                for (int j = 0; j < K - 1; ++j) {
+                    tv[j] = tv[j + 1];
+                    ti[j] = ti[j + 1];
+                }
+                tv[K - 1] = -INFINITY;
+                ti[K - 1] = INT_MAX;
+            }
+            if (tid == 0) {
+                topv[r] = bv;
+                topi[r] = bi;
+            }
+        }
+        __syncthreads();
+    };
+    constexpr int EPC = BF16 ? 8 : 4;
+    const bool vec = (reinterpret_cast<uintptr_t>(base) & 15) == 0;
+    const int nch = vec ? vocab / EPC : 0;
+    auto chunk = [&](const u32x4 &w, int c) __attribute__((always_inline)) {
+        float v[EPC];
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+            const uint32_t bits = w[BF16 ? (e >> 1) : e];
+            v[e] = BF16 ? __builtin_bit_cast(float, (e & 1) ? (bits & 0xffff0000u) : (bits << 16))
+                        : __builtin_bit_cast(float, bits);
+        }
+        lse_add(v);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) consider(v[e], c * EPC + e);
+    };
+    auto load4 = [&](u32x4 (&w)[4], int c0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c0 + u * NT) * 16);
+    };
+    int c = tid;
+    if (nch >= 4 * NT) {   // first batch, then the threshold
+        u32x4 w[4];
+        load4(w, c);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) chunk(w[u], c + u * NT);
+        c += 4 * NT;
+        merge();
+        clear_list();
+        if (tid < k) {
+            tv[0] = topv[tid];
+            ti[0] = topi[tid];
+        }
+        if (topi[k - 1] != INT_MAX) {
+            thr_v = topv[k - 1];
+            thr_i = topi[k - 1];
+        }
+    }
+    // the rest in batches of 4 chunks, the next batch loading while this one is consumed
+    u32x4 nxt[4];
+    if (c + 3 * NT < nch) load4(nxt, c);
+    for (; c + 3 * NT < nch; c += 4 * NT) {
+        u32x4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = nxt[u];
+        if (c + 7 * NT < nch) load4(nxt, c + 4 * NT);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) chunk(w[u], c + u * NT);
+    }
+    for (; c < nch; c += NT) chunk(*reinterpret_cast<const u32x4 *>(base + (size_t)c * 16), c);
+    for (int i = nch * EPC + tid; i < vocab; i += NT) {
+        const float v[1] = {logit_at<BF16>(base, i)};
+        lse_add(v);
+        consider(v[0], i);
+    }
+    // workgroup log-sum-exp: max, then the sums rescaled to it
+    __shared__ float red[NW];
+    __shared__ double dred[NW];
+    float gm = mx;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+    if ((tid & 63) == 0) red[tid >> 6] = gm;
+    __syncthreads();
+    gm = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) gm = fmaxf(gm, red[w]);
+    sum = mx == -INFINITY ? 0.0 : sum * exp((double)mx - (double)gm);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
     if ((tid & 63) == 0) dred[tid >> 6] = sum;
     __syncthreads();
     double tot = 0.0;
 #pragma unroll
-    for (int w = 0; w < NT / 64; ++w) tot += dred[w];
+    for (int w = 0; w < NW; ++w) tot += dred[w];
     const float log_sum = (float)log(tot);
-    // k merge rounds over the threads' list heads
-    __shared__ float hv[NT / 64];
-    __shared__ int hi[NT / 64];
-    for (int r = 0; r < k; ++r) {
-        float bv = tv[0];
-        int bi = ti[0];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (ranks_before(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        __syncthreads();
-        if ((tid & 63) == 0) {
-            hv[tid >> 6] = bv;
-            hi[tid >> 6] = bi;
-        }
-        __syncthreads();
-        bv = hv[0];
-        bi = hi[0];
-#pragma unroll
-        for (int w = 1; w < NT / 64; ++w)
-            if (ranks_before(hv[w], hi[w], bv, bi)) {
-                bv = hv[w];
-                bi = hi[w];
-            }
-        if (ti[0] == bi && bi != INT_MAX) {   // indices are disjoint across threads: one owner pops
-#pragma unroll
-            for (int j = 0; j < K - 1; ++j) {
-                tv[j] = tv[j + 1];
-                ti[j] = ti[j + 1];
-            }
-            tv[K - 1] = -INFINITY;
-            ti[K - 1] = INT_MAX;
-        }
-        if (tid == 0) {
-            top_idx[(size_t)row * k + r] = bi == INT_MAX ? -1 : bi;
-            top_lp[(size_t)row * k + r] = (bv - mx) - log_sum;   // log_softmax: (x - max) - log(sum)
-        }
+    merge();
+    if (tid < k) {
+        const int bi = topi[tid];
+        top_idx[(size_t)row * k + tid] = bi == INT_MAX ? -1 : bi;
+        top_lp[(size_t)row * k + tid] = (topv[tid] - gm) - log_sum;   // log_softmax: (x - max) - log(sum)
     }
 }
 
 // ---- best-first tree build, one wave per request ----
+//
+// Heap entries are (neg, depth, parent, rank, cnt), popped in tuple order.
+// (parent, rank) is unique, so cnt never decides and the order is
+// (neg, key) with key = depth << 16 | (parent + 1) << 4 | rank compared
+// unsigned.
+//
+// Sorted path (every position's log-probs non-increasing in rank, as top-k
+// output is): a parent's children have keys neg_p - lp[d][r] that are
+// non-decreasing in r (rounding is monotone) with ties to the smaller rank,
+// so they pop in rank order and only each parent's next child can be the
+// heap's minimum.  The frontier - one entry per parent with a next rank - is
+// kept sorted across the wave, lane i holding the i-th smallest entry: a pop
+// reads lane 0, and the popped entry's next sibling and the popped node's
+// first child go in by two ballots and one three-way shift.  After pop i the
+// frontier holds at most i + 2 entries and want - i - 1 pops remain, so it
+// only outgrows 64 lanes once fewer than 64 pops remain, and entries pushed
+// past lane 63 could never pop.
+// Other inputs scan the pool of every pushed candidate (up to k per node).
 
-struct Cand {
-    double neg;     // -(path log-probability)
-    int depth, parent, rank, cnt;
-};
+constexpr int kLMax = 255;
+constexpr int kPoolMax = kTopKMax * kMaxPack;   // candidates ever pushed: k * (1 + nodes)
+constexpr uint32_t kDead = 0xffffffffu;
 
-// the heap's order: smaller tuple (neg, depth, parent, rank, cnt) pops first
-__device__ __forceinline__ bool pops_before(const Cand &a, const Cand &b) {
-    if (a.neg != b.neg) return a.neg < b.neg;
-    if (a.depth != b.depth) return a.depth < b.depth;
-    if (a.parent != b.parent) return a.parent < b.parent;
-    if (a.rank != b.rank) return a.rank < b.rank;
-    return a.cnt < b.cnt;
+__device__ __forceinline__ uint32_t heap_key(int depth, int parent, int rank) {
+    return (uint32_t)depth << 16 | (uint32_t)(parent + 1) << 4 | (uint32_t)rank;
 }
 
-constexpr int kPoolMax = kTopKMax * kMaxPack;   // candidates ever pushed: k * (1 + nodes)
+// (n1, k1) pops before (n2, k2)
+__device__ __forceinline__ bool pops_before(double n1, uint32_t k1, double n2, uint32_t k2) {
+    return (n1 < n2) | ((n1 == n2) & (k1 < k2));   // bitwise: no short-circuit branches
+}
+
+// one DPP step of the argmin: combine with the lane CTRL names (lanes
+// without a source keep their own value)
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ void argmin_dpp(double &neg, uint32_t &key) {
+    const uint64_t nb = __builtin_bit_cast(uint64_t, neg);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)nb, (int)(uint32_t)nb, CTRL, ROW_MASK, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(nb >> 32), (int)(uint32_t)(nb >> 32), CTRL,
+                                                              ROW_MASK, 0xf, false);
+    const uint32_t ok = (uint32_t)__builtin_amdgcn_update_dpp((int)key, (int)key, CTRL, ROW_MASK, 0xf, false);
+    const double on = __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+    const bool take = pops_before(on, ok, neg, key);
+    neg = take ? on : neg;
+    key = take ? ok : key;
+}
+
+// the wave's minimum (neg, key), in every lane: an inclusive scan over each
+// row of 16 lanes (row_shr 1, 2, 4, 8), rows chained by row_bcast 15 and 31,
+// lane 63 read out
+__device__ __forceinline__ void wave_argmin(double &neg, uint32_t &key) {
+    argmin_dpp<0x111>(neg, key);        // row_shr:1
+    argmin_dpp<0x112>(neg, key);        // row_shr:2
+    argmin_dpp<0x114>(neg, key);        // row_shr:4
+    argmin_dpp<0x118>(neg, key);        // row_shr:8
+    argmin_dpp<0x142, 0xa>(neg, key);   // row_bcast:15 into rows 1 and 3
+    argmin_dpp<0x143, 0xc>(neg, key);   // row_bcast:31 into rows 2 and 3
+    const uint64_t nb = __builtin_bit_cast(uint64_t, neg);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)nb, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(nb >> 32), 63);
+    key = (uint32_t)__builtin_amdgcn_readlane((int)key, 63);
+    neg = __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+}
+
+// a uniform lane's double
+__device__ __forceinline__ double lane_value(double x, int lane) {
+    const uint64_t xb = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)xb, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(xb >> 32), lane);
+    return __builtin_bit_cast(double, (uint64_t)hi << 32 | lo);
+}
+
+// lane i receives lane i + 1's value (wave_shl:1; lane 63 keeps its own)
+__device__ __forceinline__ uint32_t shift_down(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x130, 0xf, 0xf, false);
+}
+__device__ __forceinline__ double shift_down(double x) {
+    const uint64_t xb = __builtin_bit_cast(uint64_t, x);
+    return __builtin_bit_cast(double, (uint64_t)shift_down((uint32_t)(xb >> 32)) << 32 | shift_down((uint32_t)xb));
+}
+// lane i receives lane i - 1's value (wave_shr:1; lane 0 keeps its own)
+__device__ __forceinline__ uint32_t shift_up(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x138, 0xf, 0xf, false);
+}
+__device__ __forceinline__ double shift_up(double x) {
+    const uint64_t xb = __builtin_bit_cast(uint64_t, x);
+    return __builtin_bit_cast(double, (uint64_t)shift_up((uint32_t)(xb >> 32)) << 32 | shift_up((uint32_t)xb));
+}
 
 template <typename LP>
 __global__ __launch_bounds__(64) void build_trees_kernel(const int64_t *__restrict__ top_idx,
@@ -164,9 +325,11 @@ __global__ __launch_bounds__(64) void build_trees_kernel(const int64_t *__restri
                                                          const int32_t *__restrict__ budget, int64_t *token,
                                                          int32_t *depth, int32_t *parent, double *score,
                                                          int32_t *n_nodes, int32_t *status) {
-    __shared__ double pneg[kPoolMax];
-    __shared__ int pmeta[kPoolMax];   // depth | parent << 8 | rank << 20 (depth < 256, parent < 4096, rank < 16)
-    __shared__ unsigned char alive[kPoolMax];
+    __shared__ double stl[kLMax * kTopKMax];   // the request's [L][k] log-probs
+    __shared__ double nscore[kMaxPack];         // popped nodes: score
+    __shared__ uint32_t nkey[kMaxPack];         // popped nodes: heap_key
+    __shared__ double pneg[kPoolMax];           // pool path: every pushed candidate
+    __shared__ uint32_t pkey[kPoolMax];
     const int b = blockIdx.x, lane = threadIdx.x;
     const int64_t *ti = top_idx + (size_t)b * L * k;
     const LP *tl = top_lp + (size_t)b * L * k;
@@ -175,64 +338,120 @@ __global__ __launch_bounds__(64) void build_trees_kernel(const int64_t *__restri
         if (lane == 0) raise_flag(status, CAST_FLAG_BAD_PACK);
         want = want < 0 ? 0 : kMaxPack - 1;
     }
+    // stage the log-probs; check that each position is sorted (NaN fails)
+    const int n_lp = L * k;
+    bool sorted = true;
+    for (int i = lane; i < n_lp; i += 64) {
+        const double v = (double)tl[i];
+        stl[i] = v;
+        if ((i % k) != k - 1) sorted = sorted && v >= (double)tl[i + 1];
+    }
+    sorted = __all(sorted);
+    __syncthreads();
+    int nodes = 0;
+    if (sorted) {
+        // lane i: the i-th smallest frontier entry (en, ek); dead entries
+        // (+inf, kDead) sort last.  Popped node j's neg and key stay in lane
+        // j & 63 of nn[j >> 6] / nk[j >> 6].
+        double en = INFINITY;
+        uint32_t ek = kDead;
+        if (lane == 0) {   // the root's first child
+            en = -stl[0];
+            ek = heap_key(1, -1, 0);
+        }
+        double nn[2] = {0.0, 0.0};
+        uint32_t nk[2] = {kDead, kDead};
+        while (nodes < want) {
+            const double bn = lane_value(en, 0);
+            const uint32_t bk = (uint32_t)__builtin_amdgcn_readlane((int)ek, 0);
+            if (bk == kDead) break;   // heap empty
+            const int me = nodes++;
+            const int d = (int)(bk >> 16), par = (int)((bk >> 4) & 0xfff) - 1, r = (int)(bk & 15);
+            // a: the popped entry's next sibling; c: the popped node's first
+            // child (uniform LDS reads, issued first; clamped in range)
+            const bool has_a = r + 1 < k, has_c = d < L;
+            const double v_a = stl[(d - 1) * k + min(r + 1, k - 1)];
+            const double v_c = stl[min(d, L - 1) * k];
+            const bool mine = lane == (me & 63);
+            nn[0] = mine && me < 64 ? bn : nn[0];
+            nk[0] = mine && me < 64 ? bk : nk[0];
+            nn[1] = mine && me >= 64 ? bn : nn[1];
+            nk[1] = mine && me >= 64 ? bk : nk[1];
+            const double pn = lane_value(par < 64 ? nn[0] : nn[1], par & 63);   // the parent's neg
+            double an = !has_a ? INFINITY : par < 0 ? -v_a : pn - v_a;   // roots push -lp, children neg_p - lp
+            uint32_t ak = has_a ? heap_key(d, par, r + 1) : kDead;
+            double cn = has_c ? bn - v_c : INFINITY;
+            uint32_t ck = has_c ? heap_key(d + 1, me, 0) : kDead;
+            const bool swap = pops_before(cn, ck, an, ak);
+            const double n_lo = swap ? cn : an, n_hi = swap ? an : cn;
+            const uint32_t k_lo = swap ? ck : ak, k_hi = swap ? ak : ck;
+            // new positions: lo at pa, hi at pb + 1, counting the old entries 1..63 before each
+            const int pa = __popcll(__ballot(lane >= 1 && pops_before(en, ek, n_lo, k_lo)));
+            const int pb = __popcll(__ballot(lane >= 1 && pops_before(en, ek, n_hi, k_hi)));
+            const double up_n = shift_down(en), dn_n = shift_up(en);
+            const uint32_t up_k = shift_down(ek), dn_k = shift_up(ek);
+            const bool s_up = lane < pa, s_lo = lane == pa, s_keep = lane <= pb, s_hi = lane == pb + 1;
+            en = s_up ? up_n : s_lo ? n_lo : s_keep ? en : s_hi ? n_hi : dn_n;
+            ek = s_up ? up_k : s_lo ? k_lo : s_keep ? ek : s_hi ? k_hi : dn_k;
+        }
+        // the nodes to LDS for the write-out below
+        for (int j = 0; j < 2; ++j)
+            if (j * 64 + lane < nodes) {
+                nscore[j * 64 + lane] = -nn[j];
+                nkey[j * 64 + lane] = nk[j];
+            }
+    } else {
+        int cnt = 0;
+        for (int r = lane; r < k; r += 64) {
+            pneg[r] = -stl[r];
+            pkey[r] = heap_key(1, -1, r);
+        }
+        cnt = k;
+        while (nodes < want) {
+            __syncthreads();
+            double bn = INFINITY;
+            uint32_t bk = kDead;
+            int bc = -1;
+            for (int c = lane; c < cnt; c += 64) {
+                if (pkey[c] != kDead && pops_before(pneg[c], pkey[c], bn, bk)) {
+                    bn = pneg[c];
+                    bk = pkey[c];
+                    bc = c;
+                }
+            }
+            wave_argmin(bn, bk);
+            if (bk == kDead) break;   // heap empty
+            const int me = nodes++;
+            const int d = (int)(bk >> 16);
+            if (lane == 0) {
+                nscore[me] = -bn;
+                nkey[me] = bk;
+            }
+            if (bc >= 0 && pkey[bc] == bk) pkey[bc] = kDead;   // (parent, rank) is unique: one owner
+            if (d < L) {
+                // the reference pushes neg - lp[d][r2] for r2 in rank order
+                for (int r = lane; r < k && cnt + r < kPoolMax; r += 64) {
+                    pneg[cnt + r] = bn - stl[d * k + r];
+                    pkey[cnt + r] = heap_key(d + 1, me, r);
+                }
+                cnt += k;
+                if (cnt > kPoolMax) cnt = kPoolMax;
+            }
+        }
+    }
+    __syncthreads();
+    // write the nodes out in pop order
     int64_t *tok_o = token + (size_t)b * (kMaxPack - 1);
     int32_t *dep_o = depth + (size_t)b * (kMaxPack - 1);
     int32_t *par_o = parent + (size_t)b * (kMaxPack - 1);
     double *sc_o = score + (size_t)b * (kMaxPack - 1);
-    // the k roots' children: depth 1, parent -1 (stored as parent + 1)
-    int cnt = 0;
-    if (lane < k) {
-        pneg[lane] = -(double)tl[lane];
-        pmeta[lane] = 1 | (0 << 8) | (lane << 20);
-        alive[lane] = 1;
-    }
-    cnt = k;
-    int nodes = 0;
-    while (nodes < want) {
-        // wave argmin over the alive candidates
-        Cand best;
-        best.neg = DBL_MAX;
-        best.depth = INT_MAX;
-        best.parent = INT_MAX;
-        best.rank = INT_MAX;
-        best.cnt = INT_MAX;
-        __syncthreads();
-        for (int c = lane; c < cnt; c += 64) {
-            if (!alive[c]) continue;
-            const int m = pmeta[c];
-            const Cand x{pneg[c], m & 0xff, ((m >> 8) & 0xfff) - 1, m >> 20, c};
-            if (pops_before(x, best)) best = x;
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            Cand o;
-            o.neg = __shfl_xor(best.neg, off);
-            o.depth = __shfl_xor(best.depth, off);
-            o.parent = __shfl_xor(best.parent, off);
-            o.rank = __shfl_xor(best.rank, off);
-            o.cnt = __shfl_xor(best.cnt, off);
-            if (pops_before(o, best)) best = o;
-        }
-        if (best.cnt == INT_MAX) break;   // heap empty
-        const int me = nodes++;
-        const int d = best.depth, r = best.rank;
-        if (lane == 0) {
-            alive[best.cnt] = 0;
-            tok_o[me] = ti[(size_t)(d - 1) * k + r];
-            dep_o[me] = d;
-            par_o[me] = best.parent;
-            sc_o[me] = -best.neg;
-        }
-        if (d < L) {
-            // children: the reference pushes neg - top_lp[d, r2] for r2 in rank order
-            if (lane < k && cnt + lane < kPoolMax) {
-                pneg[cnt + lane] = best.neg - (double)tl[(size_t)d * k + lane];
-                pmeta[cnt + lane] = (d + 1) | ((me + 1) << 8) | (lane << 20);
-                alive[cnt + lane] = 1;
-            }
-            cnt += k;
-            if (cnt > kPoolMax) cnt = kPoolMax;
-        }
+    for (int i = lane; i < nodes; i += 64) {
+        const uint32_t key = nkey[i];
+        const int d = (int)(key >> 16), r = (int)(key & 15);
+        tok_o[i] = ti[(d - 1) * k + r];
+        dep_o[i] = d;
+        par_o[i] = (int)((key >> 4) & 0xfff) - 1;
+        sc_o[i] = nscore[i];
     }
     if (lane == 0) n_nodes[b] = nodes;
 }
@@ -248,10 +467,14 @@ extern "C" int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t ro
     if (rows == 0) return CAST_OK;
     if (!logits || !top_idx || !top_lp) return CAST_ERR_NULL_POINTER;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (dtype == CAST_BF16)
-        draft_topk_kernel<true><<<rows, 256, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+    if (dtype == CAST_BF16 && k <= 8)
+        draft_topk_kernel<true, 8><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+    else if (dtype == CAST_BF16)
+        draft_topk_kernel<true, kTopKMax><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+    else if (k <= 8)
+        draft_topk_kernel<false, 8><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
     else
-        draft_topk_kernel<false><<<rows, 256, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+        draft_topk_kernel<false, kTopKMax><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
     return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
 }
 
@@ -259,7 +482,7 @@ extern "C" int cast_build_trees(const int64_t *top_idx, const void *top_lp, int3
                                 int32_t L, int32_t k, const int32_t *budget, int64_t *token, int32_t *depth,
                                 int32_t *parent, double *score, int32_t *n_nodes, int32_t *status,
                                 cast_stream_t stream) {
-    if (batch < 0 || L < 1 || L > 255 || k < 1 || k > kTopKMax) return CAST_ERR_SHAPE;
+    if (batch < 0 || L < 1 || L > kLMax || k < 1 || k > kTopKMax) return CAST_ERR_SHAPE;
     if (lp_dtype != CAST_FP32 && lp_dtype != CAST_FP64) return CAST_ERR_DTYPE;
     if (batch == 0) return CAST_OK;
     if (!top_idx || !top_lp || !budget || !token || !depth || !parent || !score || !n_nodes)

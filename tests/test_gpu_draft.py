@@ -40,6 +40,33 @@ def test_topk_marginals_match_oracle(gpu, dtype, k):
     assert hi.device.type == "cpu" and torch.equal(hi, idx.cpu())
 
 
+@pytest.mark.parametrize("dtype,V,pad", [(torch.float32, 151936, 0), (torch.bfloat16, 151936, 0),
+                                         (torch.bfloat16, 1000, 3), (torch.float32, 50000, 1)])
+def test_topk_marginals_edge_rows(gpu, dtype, V, pad):
+    # all-equal, increasing, decreasing, mostly -inf and integer-tied rows;
+    # small vocabularies and unaligned row strides take the scalar path
+    from cast_amd.draft import topk_marginals
+    rng = np.random.default_rng(V + pad)
+    x = np.empty((6, V + pad), dtype=np.float32)
+    x[0] = 0.0
+    x[1] = np.arange(V + pad) / 7.0
+    x[2] = -np.arange(V + pad) / 7.0
+    x[3] = -np.inf
+    x[3, rng.integers(0, V, size=5)] = rng.normal(size=5)
+    x[4] = np.round(rng.normal(scale=3.0, size=V + pad))
+    x[5] = rng.normal(size=V + pad)
+    xd = torch.from_numpy(x).to(gpu).to(dtype)[:, :V]
+    print(f"case topk-edge {dtype} V={V} ld={xd.stride(0)}", flush=True)
+    for k in (1, 8, 16):
+        idx, lp = topk_marginals(xd, k, on_device=True)
+        want_i, want_lp = OD.topk_log_softmax(xd.float().cpu().numpy(), k)
+        assert idx.cpu().numpy().tolist() == want_i.tolist(), f"k={k}"
+        got = lp.cpu().numpy()
+        assert np.array_equal(np.isinf(got), np.isinf(want_lp))
+        fin = np.isfinite(want_lp)
+        assert np.abs(got[fin] - want_lp[fin]).max() <= 2e-5, f"k={k}"
+
+
 def test_build_trees_match_reference_fixtures(gpu):
     from cast_amd.draft import build_trees
     cases = [c for c in FIX["cases"] if "127" in c["trees"]]
@@ -86,3 +113,33 @@ def test_device_draft_pipeline_matches_oracle_heap(gpu):
         assert got == [(t, d, p, s) for t, d, p, s in want]
     nodes = build_tree_device(idx_h[2], lp_h[2], 127)
     assert [(n.token, n.depth, n.parent, n.score) for n in nodes] == OD.build_tree(idx_h[2], lp_h[2], 127)
+
+
+@pytest.mark.parametrize("case", ["unsorted", "ties-sorted", "ties-unsorted", "one-position", "neg-inf-tails",
+                                  "deep-k2", "k16-long"])
+def test_build_trees_paths_match_oracle_heap(gpu, case):
+    # sorted positions take the frontier search, others the full pool scan;
+    # both must pop exactly the oracle heap's order, ties and -inf included
+    from cast_amd.draft import build_trees
+    rng = np.random.default_rng(sum(map(ord, case)))
+    L, k, B = {"one-position": (1, 4, 3), "deep-k2": (255, 2, 3), "k16-long": (40, 16, 3)}.get(case, (15, 8, 4))
+    lp = -np.abs(rng.normal(scale=2.0, size=(B, L, k)))
+    if case.startswith("ties"):
+        lp = np.round(lp * 2) / 2                          # many equal scores and sums
+    lp = -np.sort(-lp, axis=-1)                            # non-increasing per position
+    if case == "neg-inf-tails":
+        lp[:, :, 5:] = -np.inf
+    if case.endswith("unsorted"):
+        lp = np.take_along_axis(lp, rng.permuted(np.tile(np.arange(k), (B, L, 1)), axis=-1), axis=-1)
+    lp = lp.astype(np.float32)
+    idx = rng.integers(0, 151936, size=(B, L, k))
+    budgets = [127, 40, 1, 0][:B]
+    print(f"case build-trees {case} L={L} k={k}", flush=True)
+    token, depth, parent, score, n_nodes = build_trees(torch.from_numpy(idx).to(gpu), torch.from_numpy(lp).to(gpu),
+                                                       torch.tensor(budgets, device=gpu), check=True)
+    for b in range(B):
+        want = OD.build_tree(idx[b], lp[b], budgets[b], k)
+        m = int(n_nodes[b])
+        got = list(zip(token[b, :m].tolist(), depth[b, :m].tolist(), parent[b, :m].tolist(),
+                       score[b, :m].tolist()))
+        assert got == [(int(t), d, p, s) for t, d, p, s in want], f"{case} request {b}"
