@@ -271,11 +271,13 @@ def draft_trees(dev, steps, warmup):
     idx, lp = topk_marginals(x, 8, on_device=True)
     t_k = time_kernel(lambda: topk_marginals(x, 8, on_device=True), steps, warmup)
     t_t = time_kernel(lambda: build_trees(idx.view(B, L, 8), lp.view(B, L, 8), bud), steps, warmup)
+    t_tt = time_kernel(lambda: torch.topk(torch.nn.functional.log_softmax(x.float(), dim=-1), 8, dim=-1), steps,
+                       warmup)
     t_r = time_kernel(reference_flow, max(3, steps // 5), 2)
     log(f"  draft trees (B={B}, 127 nodes): device {t_d:.1f} us (top-k {t_k:.1f}, trees {t_t:.1f}), "
-        f"torch topk + host heap {t_r:.1f} us")
+        f"torch topk + host heap {t_r:.1f} us (torch log_softmax + topk alone {t_tt:.1f} us)")
     return dict(device_us=round(t_d, 2), topk_us=round(t_k, 2), trees_us=round(t_t, 2),
-                torch_topk_host_heap_us=round(t_r, 2), batch=B, nodes=127,
+                torch_topk_host_heap_us=round(t_r, 2), torch_log_softmax_topk_us=round(t_tt, 2), batch=B, nodes=127,
                 topk_gbps=round(B * L * V * 2 / (t_k * 1e-6) / 1e9, 1))
 
 

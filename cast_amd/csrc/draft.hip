@@ -20,11 +20,6 @@ namespace cast {
 
 constexpr int kTopKMax = 16;
 
-// (v1, i1) ranks before (v2, i2): larger value, then smaller index.
-__device__ __forceinline__ bool ranks_before(float v1, int i1, float v2, int i2) {
-    return v1 > v2 || (v1 == v2 && i1 < i2);
-}
-
 template <bool BF16>
 __device__ __forceinline__ float logit_at(const char *row, int i) {
     if constexpr (BF16)
@@ -33,54 +28,92 @@ __device__ __forceinline__ float logit_at(const char *row, int i) {
         return reinterpret_cast<const float *>(row)[i];
 }
 
+// Rank keys: (value, index) pairs as one unsigned 64-bit integer whose order
+// is the ranking order (larger value first, equal values by smaller index):
+// the value's order-preserving bits (-0 folded into +0) above the complement
+// of the index.  NaN maps to 0, the empty key, which never ranks.
+__device__ __forceinline__ uint64_t rank_key(float v, int i) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);   // -0 + 0 = +0
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return v == v ? (uint64_t)ord << 32 | (uint32_t)~(uint32_t)i : 0;
+}
+__device__ __forceinline__ float key_value(uint64_t key) {
+    const uint32_t ord = (uint32_t)(key >> 32);
+    return __builtin_bit_cast(float, (ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+__device__ __forceinline__ int key_index(uint64_t key) { return (int)~(uint32_t)key; }
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint64_t key_max_dpp(uint64_t key) {   // lanes without a source keep their own
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)key, (int)(uint32_t)key, CTRL, ROW_MASK,
+                                                              0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(key >> 32), (int)(uint32_t)(key >> 32),
+                                                              CTRL, ROW_MASK, 0xf, false);
+    const uint64_t o = (uint64_t)hi << 32 | lo;
+    return o > key ? o : key;
+}
+__device__ __forceinline__ uint64_t lane_key(uint64_t key, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(key >> 32), lane);
+    return (uint64_t)hi << 32 | lo;
+}
+// the wave's largest key, in every lane
+__device__ __forceinline__ uint64_t wave_key_max(uint64_t key) {
+    key = key_max_dpp<0x111>(key);        // row_shr:1
+    key = key_max_dpp<0x112>(key);        // row_shr:2
+    key = key_max_dpp<0x114>(key);        // row_shr:4
+    key = key_max_dpp<0x118>(key);        // row_shr:8
+    key = key_max_dpp<0x142, 0xa>(key);   // row_bcast:15 into rows 1 and 3
+    key = key_max_dpp<0x143, 0xc>(key);   // row_bcast:31 into rows 2 and 3
+    return lane_key(key, 63);
+}
+// the largest key of lanes 0..15, in every lane
+__device__ __forceinline__ uint64_t row_key_max(uint64_t key) {
+    key = key_max_dpp<0x111>(key);
+    key = key_max_dpp<0x112>(key);
+    key = key_max_dpp<0x114>(key);
+    key = key_max_dpp<0x118>(key);
+    return lane_key(key, 15);
+}
+
 // One workgroup per row: top-k (value, index) and the row's log-sum-exp.
 //
-// Each thread keeps its best K elements (K >= k) in a fully unrolled sorted
-// list; k merge rounds of the list heads give the row's top k.  After the
-// first batch (4 chunks of 16 bytes per thread) one merge finds the top k so
-// far; its k-th entry is a threshold no final top-k element ranks after, so
-// later elements that do not rank before it skip the list (the filter is
-// exact), and the merged entries are dealt back one per thread.
+// Each thread keeps its best K rank keys (K >= k) in a fully unrolled sorted
+// list; k merge rounds of the list heads give the row's top k.  Only
+// elements whose key is at least a threshold key enter the lists.  The
+// threshold comes from the first batch (4 chunks of 16 bytes per thread):
+// the k-th largest of the threads' best keys, a bound no final top-k element
+// falls below since k real elements are at or above it.  A chunk whose max
+// is below the threshold's value skips the per-element test.
 //
 // Log-sum-exp: per 16-byte chunk, the chunk's max updates the thread's
-// running max, the chunk's exp terms are summed in float and the thread's
-// total is rescaled and accumulated in double.
+// running max, the chunk's exp terms are summed pairwise in float and the
+// thread's total is rescaled and accumulated in double.
 template <bool BF16, int K>
 __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict__ logits, int64_t ld, int32_t vocab,
                                                          int32_t k, int64_t *__restrict__ top_idx,
                                                          float *__restrict__ top_lp) {
     constexpr int NT = 512, NW = NT / 64;
     constexpr float kLog2e = 1.4426950408889634f;
-    const int row = blockIdx.x, tid = threadIdx.x;
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const char *base = static_cast<const char *>(logits) + (size_t)row * (size_t)ld * (BF16 ? 2 : 4);
-    float tv[K];
-    int ti[K];
-    auto clear_list = [&]() __attribute__((always_inline)) {
+    uint64_t tk[K];   // descending; 0 = empty
 #pragma unroll
-        for (int j = 0; j < K; ++j) {
-            tv[j] = -INFINITY;
-            ti[j] = INT_MAX;   // empty slot
-        }
-    };
-    clear_list();
-    float thr_v = -INFINITY;   // elements must rank before (thr_v, thr_i)
-    int thr_i = INT_MAX;
-    // a thread's elements come in increasing index order, so a new element
-    // goes behind equal values already in its list
-    auto consider = [&](float v, int i) __attribute__((always_inline)) {
-        if ((v > tv[K - 1] || ti[K - 1] == INT_MAX) && ranks_before(v, i, thr_v, thr_i)) {
+    for (int j = 0; j < K; ++j) tk[j] = 0;
+    uint64_t thr = 1;           // every key but NaN's passes
+    float thr_v = -INFINITY;    // the threshold's value and index: an element passes
+    int thr_i = INT_MAX;        // if v > thr_v, or v == thr_v and its index <= thr_i
+    auto insert = [&](uint64_t key) __attribute__((always_inline)) {   // keys are unique
+        if (key > tk[K - 1]) {
             bool placed = false;
 #pragma unroll
             for (int j = K - 1; j >= 0; --j) {
-                const bool stays_ahead = j > 0 && !(v > tv[j - 1] || ti[j - 1] == INT_MAX);
                 if (!placed) {
-                    if (j == 0 || stays_ahead) {
-                        tv[j] = v;
-                        ti[j] = i;
+                    if (j == 0 || key < tk[j - 1]) {
+                        tk[j] = key;
                         placed = true;
                     } else {
-                        tv[j] = tv[j - 1];
-                        ti[j] = ti[j - 1];
+                        tk[j] = tk[j - 1];
                     }
                 }
             }
@@ -88,101 +121,115 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
     };
     float mx = -INFINITY;   // running max; sum holds sum(exp(x - mx))
     double sum = 0.0;
-    auto lse_add = [&](const auto &v) __attribute__((always_inline)) {
+    auto lse_add = [&](const auto &v, float m) __attribute__((always_inline)) {   // m = max(v)
         constexpr int n = sizeof(v) / sizeof(float);
-        float m = v[0];
-#pragma unroll
-        for (int e = 1; e < n; ++e) m = fmaxf(m, v[e]);
         const float nm = fmaxf(mx, m);
         const float ref = nm == -INFINITY ? 0.f : nm;
-        float part = 0.f;
+        float ex[n];
 #pragma unroll
-        for (int e = 0; e < n; ++e) part += __builtin_amdgcn_exp2f((v[e] - ref) * kLog2e);
-        sum = sum * (double)__builtin_amdgcn_exp2f((mx - ref) * kLog2e) + (double)part;
+        for (int e = 0; e < n; ++e) ex[e] = __builtin_amdgcn_exp2f((v[e] - ref) * kLog2e);
+#pragma unroll
+        for (int w = 1; w < n; w *= 2)   // pairwise
+#pragma unroll
+            for (int e = 0; e + w < n; e += 2 * w) ex[e] += ex[e + w];
+        sum = sum * (double)__builtin_amdgcn_exp2f((mx - ref) * kLog2e) + (double)ex[0];
         mx = nm;
     };
-    // k rounds over the list heads; the row's top k so far, in order, into topv/topi
-    __shared__ float hv[NW], topv[K];
-    __shared__ int hi[NW], topi[K];
+    // k rounds over the list heads: the k largest keys of all lists, in
+    // order, into topk (the popped heads leave their lists); one barrier per
+    // round, the per-wave maxima double-buffered by round parity
+    __shared__ uint64_t wmax[2][NW], topk[K];
     auto merge = [&]() __attribute__((always_inline)) {
         for (int r = 0; r < k; ++r) {
-            float bv = tv[0];
-            int bi = ti[0];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const int oi = __shfl_xor(bi, off);
-                if (ranks_before(ov, oi, bv, bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
+            uint64_t best = wave_key_max(tk[0]);
+            if (lane == 0) wmax[r & 1][wv] = best;
             __syncthreads();
-            if ((tid & 63) == 0) {
-                hv[tid >> 6] = bv;
-                hi[tid >> 6] = bi;
-            }
-            __syncthreads();
-            bv = hv[0];
-            bi = hi[0];
+            best = row_key_max(lane < NW ? wmax[r & 1][lane] : 0);
+            if (tk[0] == best && best != 0) {   // keys are unique: one owner pops
 #pragma unroll
-            for (int w = 1; w < NW; ++w)
-                if (ranks_before(hv[w], hi[w], bv, bi)) {
-                    bv = hv[w];
-                    bi = hi[w];
-                }
-            if (ti[0] == bi && bi != INT_MAX) {   // indices are disjoint across threads: one owner pops
-#pragma unroll
-                for (int j = 0; j < K - 1; ++j) {
-                    tv[j] = tv[j + 1];
-                    ti[j] = ti[j + 1];
-                }
-                tv[K - 1] = -INFINITY;
-                ti[K - 1] = INT_MAX;
+                for (int j = 0; j < K - 1; ++j) tk[j] = tk[j + 1];
+                tk[K - 1] = 0;
             }
-            if (tid == 0) {
-                topv[r] = bv;
-                topi[r] = bi;
-            }
+            if (tid == 0) topk[r] = best;
         }
         __syncthreads();
     };
     constexpr int EPC = BF16 ? 8 : 4;
     const bool vec = (reinterpret_cast<uintptr_t>(base) & 15) == 0;
     const int nch = vec ? vocab / EPC : 0;
-    auto chunk = [&](const u32x4 &w, int c) __attribute__((always_inline)) {
-        float v[EPC];
+    auto unpack = [&](const u32x4 &w, float (&v)[EPC]) __attribute__((always_inline)) {
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
             const uint32_t bits = w[BF16 ? (e >> 1) : e];
             v[e] = BF16 ? __builtin_bit_cast(float, (e & 1) ? (bits & 0xffff0000u) : (bits << 16))
                         : __builtin_bit_cast(float, bits);
         }
-        lse_add(v);
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) consider(v[e], c * EPC + e);
     };
-    auto load4 = [&](u32x4 (&w)[4], int c0) {
+    auto chunk_max = [&](const float (&v)[EPC]) __attribute__((always_inline)) {
+        float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if constexpr (EPC == 8) m = fmaxf(m, fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+        return m;
+    };
+    // the chunk's elements that pass, in index order, one insertion sequence for all
+    auto filter = [&](const float (&v)[EPC], float m, int c) __attribute__((always_inline)) {
+        if (m >= thr_v) {   // no element of the chunk passes otherwise
+            uint32_t pm = 0;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e)
+                pm |= ((v[e] > thr_v) | ((v[e] == thr_v) & (c * EPC + e <= thr_i)) ? 1u : 0u) << e;
+            while (pm) {
+                const int e = __builtin_ctz(pm);
+                pm &= pm - 1;
+                float ve = v[0];
+#pragma unroll
+                for (int e2 = 1; e2 < EPC; ++e2) ve = e == e2 ? v[e2] : ve;
+                insert(rank_key(ve, c * EPC + e));
+            }
+        }
+    };
+    auto chunk = [&](const u32x4 &w, int c) __attribute__((always_inline)) {
+        float v[EPC];
+        unpack(w, v);
+        const float m = chunk_max(v);
+        lse_add(v, m);
+        filter(v, m, c);
+    };
+    auto load4 = [&](u32x4 (&w)[4], int c0) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c0 + u * NT) * 16);
     };
     int c = tid;
-    if (nch >= 4 * NT) {   // first batch, then the threshold
+    if (nch >= 4 * NT) {   // first batch: the threshold, then the batch through it
         u32x4 w[4];
         load4(w, c);
+        uint64_t best = 0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) chunk(w[u], c + u * NT);
-        c += 4 * NT;
+        for (int u = 0; u < 4; ++u) {
+            float v[EPC];
+            unpack(w[u], v);
+            const float m = chunk_max(v);
+            lse_add(v, m);
+            int fi = EPC - 1;   // the chunk's first element equal to its max
+#pragma unroll
+            for (int e = EPC - 2; e >= 0; --e) fi = v[e] == m ? e : fi;
+            const uint64_t key = rank_key(m, (c + u * NT) * EPC + fi);
+            best = key > best ? key : best;
+        }
+        tk[0] = best;
         merge();
-        clear_list();
-        if (tid < k) {
-            tv[0] = topv[tid];
-            ti[0] = topi[tid];
+        if (topk[k - 1] != 0) {
+            thr = topk[k - 1];
+            thr_v = key_value(thr);
+            thr_i = key_index(thr);
         }
-        if (topi[k - 1] != INT_MAX) {
-            thr_v = topv[k - 1];
-            thr_i = topi[k - 1];
+        tk[0] = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float v[EPC];
+            unpack(w[u], v);
+            filter(v, chunk_max(v), c + u * NT);
         }
+        c += 4 * NT;
     }
     // the rest in batches of 4 chunks, the next batch loading while this one is consumed
     u32x4 nxt[4];
@@ -198,8 +245,9 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
     for (; c < nch; c += NT) chunk(*reinterpret_cast<const u32x4 *>(base + (size_t)c * 16), c);
     for (int i = nch * EPC + tid; i < vocab; i += NT) {
         const float v[1] = {logit_at<BF16>(base, i)};
-        lse_add(v);
-        consider(v[0], i);
+        lse_add(v, v[0]);
+        const uint64_t key = rank_key(v[0], i);
+        if (key >= thr) insert(key);
     }
     // workgroup log-sum-exp: max, then the sums rescaled to it
     __shared__ float red[NW];
@@ -207,7 +255,7 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
     float gm = mx;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
-    if ((tid & 63) == 0) red[tid >> 6] = gm;
+    if (lane == 0) red[wv] = gm;
     __syncthreads();
     gm = red[0];
 #pragma unroll
@@ -215,7 +263,7 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
     sum = mx == -INFINITY ? 0.0 : sum * exp((double)mx - (double)gm);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if ((tid & 63) == 0) dred[tid >> 6] = sum;
+    if (lane == 0) dred[wv] = sum;
     __syncthreads();
     double tot = 0.0;
 #pragma unroll
@@ -223,9 +271,9 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
     const float log_sum = (float)log(tot);
     merge();
     if (tid < k) {
-        const int bi = topi[tid];
-        top_idx[(size_t)row * k + tid] = bi == INT_MAX ? -1 : bi;
-        top_lp[(size_t)row * k + tid] = (topv[tid] - gm) - log_sum;   // log_softmax: (x - max) - log(sum)
+        const uint64_t key = topk[tid];
+        top_idx[(size_t)row * k + tid] = key == 0 ? -1 : key_index(key);
+        top_lp[(size_t)row * k + tid] = key == 0 ? NAN : (key_value(key) - gm) - log_sum;   // (x - max) - log(sum)
     }
 }
 
