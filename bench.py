@@ -326,6 +326,8 @@ def main():
     ap.add_argument("--kv-split", type=int, default=0, help="keys per split-K chunk (0: library choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--only", choices=["kv_append", "draft_trees", "store_layout"],
+                    help="only run one secondary workload (for kernel profiles); prints its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches), to scale HBM byte counters")
     args = ap.parse_args()
@@ -349,6 +351,10 @@ def main():
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
+        return
+    if args.only:
+        fn = {"kv_append": kv_append, "draft_trees": draft_trees, "store_layout": store_layout}[args.only]
+        print(json.dumps({args.only: fn(dev, args.steps, args.warmup)}), flush=True)
         return
     log(f"device: {torch.cuda.get_device_name(dev)}")
     wl = scenarios.qwen3_headline()

@@ -156,31 +156,23 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
 
 # ---- accepted-path KV append (cast_trees/serving.py:264-289)
 
-_PTR_TABLES = {}    # (device, addresses) -> device int64 table, reused while the buffers stay put
+_APPEND_LAYOUTS = {}   # (id, address) of every per-layer tensor -> (weakrefs, checked layout)
 
 
-def _pointer_table(dev, addrs):
-    """Device array of per-layer base addresses.  Built (one host-to-device
-    copy) only when the addresses change, i.e. after the stores or the pack
-    buffers were reallocated."""
-    key = (str(dev), tuple(addrs))
-    t = _PTR_TABLES.get(key)
-    if t is None:
-        if len(_PTR_TABLES) > 8:
-            _PTR_TABLES.clear()
-        t = _PTR_TABLES[key] = torch.tensor(addrs, dtype=torch.int64, device=dev)
-    return t
-
-
-def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_len, new_len, status=None):
-    """One cast_store_append launch over every layer (all arguments device
-    tensors; buf_* / pack_* lists of per-layer tensors)."""
-    from . import _lib
-    from .tree_attn import _DTYPES
-    lib = _lib.load()
+def _append_layout(buf_k, buf_v, pack_k, pack_v):
+    """Check the per-layer stores and packs once and build the device table
+    of their base addresses.  The result is reused while the same tensor
+    objects sit at the same addresses (weak references tell a live object
+    from a new one that got a freed object's id), so a decode loop that keeps
+    its buffers pays the per-layer checks and the table copy once."""
     L = len(buf_k)
     if not (len(buf_v) == len(pack_k) == len(pack_v) == L) or L == 0:
         raise ValueError("one store and one pack K/V tensor per layer")
+    tensors = (*pack_k, *pack_v, *buf_k, *buf_v)
+    key = tuple((id(t), t.data_ptr()) for t in tensors)
+    hit = _APPEND_LAYOUTS.get(key)
+    if hit is not None and all(r() is t for r, t in zip(hit[0], tensors)):
+        return hit[1]
     k0, p0 = buf_k[0], pack_k[0]
     B, Hkv, cap, D = (int(x) for x in k0.shape)
     total_q = int(p0.shape[1])
@@ -194,19 +186,38 @@ def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_
             raise ValueError("pack K/V need a contiguous, 16-byte aligned head dim")
     if k0.stride(-1) != 1 or any(t.data_ptr() % 16 for t in (*buf_k, *buf_v)):
         raise ValueError("the store needs a contiguous, 16-byte aligned head dim")
+    for t in tensors:
+        if t.device != k0.device:
+            raise ValueError("stores and packs must be on one device")
+    ptrs = torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=k0.device)
+    layout = dict(ptrs=ptrs, L=L, B=B, Hkv=Hkv, cap=cap, D=D, total_q=total_q, dtype=k0.dtype, device=k0.device,
+                  pack_k=(p0.stride(1), p0.stride(0)), pack_v=(pack_v[0].stride(1), pack_v[0].stride(0)),
+                  store_k=tuple(k0.stride()[:3]), store_v=tuple(buf_v[0].stride()[:3]))
+    if len(_APPEND_LAYOUTS) >= 8:
+        _APPEND_LAYOUTS.clear()
+    _APPEND_LAYOUTS[key] = (tuple(weakref.ref(t) for t in tensors), layout)
+    return layout
+
+
+def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_len, new_len, status=None):
+    """One cast_store_append launch over every layer (all arguments device
+    tensors; buf_* / pack_* lists of per-layer tensors)."""
+    from . import _lib
+    from .tree_attn import _DTYPES
+    lib = _lib.load()
+    lay = _append_layout(buf_k, buf_v, pack_k, pack_v)
+    L, B = lay["L"], lay["B"]
     n = int(src_row.shape[0])
     if n > B or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
         raise ValueError("path must be [B, >=128] (as written by greedy_accept) for B <= the store batch")
-    dev = k0.device
-    ptrs = _pointer_table(dev, [t.data_ptr() for t in (*pack_k, *pack_v, *buf_k, *buf_v)])
+    ptrs = lay["ptrs"]
     pk, pv, sk, sv = (ptrs[i * L:(i + 1) * L] for i in range(4))
-    with torch.cuda.device(dev):
+    with torch.cuda.device(lay["device"]):
         st = lib.cast_store_append(
             _lib.ptr(pk), _lib.ptr(pv), _lib.ptr(sk), _lib.ptr(sv), L, _lib.ptr(src_row), _lib.ptr(path),
-            path.stride(0), _lib.ptr(path_len), _lib.ptr(store_len), _lib.ptr(new_len), n, total_q, cap, Hkv, D,
-            p0.stride(1), p0.stride(0), pack_v[0].stride(1), pack_v[0].stride(0), k0.stride(0), k0.stride(1),
-            k0.stride(2), buf_v[0].stride(0), buf_v[0].stride(1), buf_v[0].stride(2), _DTYPES[k0.dtype],
-            _lib.ptr(status), _lib.stream_of(k0))
+            path.stride(0), _lib.ptr(path_len), _lib.ptr(store_len), _lib.ptr(new_len), n, lay["total_q"],
+            lay["cap"], lay["Hkv"], lay["D"], *lay["pack_k"], *lay["pack_v"], *lay["store_k"], *lay["store_v"],
+            _DTYPES[lay["dtype"]], _lib.ptr(status), _lib.stream_of(buf_k[0]))
     _lib.check(st, "cast_store_append")
 
 

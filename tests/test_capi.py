@@ -116,3 +116,24 @@ def test_store_append_host_validation(lib):
     assert f(*args(stride=64)) == 7              # path rows narrower than 128
     assert f(*args(dtype=3)) == 4                # dtype
     assert f(*args(B=0)) == 0 and f(*args(layers=0)) == 0
+
+
+def test_append_layout_checked_once_and_rechecked_on_change():
+    # the per-layer checks of the KV append run once per set of buffers; a
+    # replaced layer tensor (new object, other shape) is checked again
+    import torch
+    from cast_amd import serving
+    L = 4
+    buf_k = [torch.empty((2, 2, 16, 64), dtype=torch.bfloat16) for _ in range(L)]
+    buf_v = [torch.empty_like(x) for x in buf_k]
+    pack_k = [torch.empty((2, 5, 64), dtype=torch.bfloat16) for _ in range(L)]
+    pack_v = [torch.empty_like(x) for x in pack_k]
+    first = serving._append_layout(buf_k, buf_v, pack_k, pack_v)
+    assert serving._append_layout(buf_k, buf_v, pack_k, pack_v) is first
+    assert first["ptrs"].tolist() == [t.data_ptr() for t in (*pack_k, *pack_v, *buf_k, *buf_v)]
+    buf_k[2] = torch.empty((2, 2, 8, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="share shape"):
+        serving._append_layout(buf_k, buf_v, pack_k, pack_v)
+    buf_k[2] = torch.empty((2, 2, 16, 64), dtype=torch.bfloat16)
+    again = serving._append_layout(buf_k, buf_v, pack_k, pack_v)
+    assert again is not first and again["ptrs"][L * 2 + 2].item() == buf_k[2].data_ptr()
