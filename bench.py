@@ -242,6 +242,48 @@ def kv_append(dev, steps, warmup, layers=36):
     return dict(fused_us=round(t_f, 2), per_layer_indexing_us=round(t_r, 2), layers=layers, rows=len(src))
 
 
+def cache_gather(dev, steps, warmup, layers=36):
+    """The batch-one decoder's accepted-path cache compaction (cast_trees/
+    verify.py:48-60) at Qwen3-8B shapes: 36 layers, 8 KV heads, D=128, bf16,
+    a cached prefix of 4096 plus a packed pass of 128, 6 kept entries.  In
+    place on the device (one launch) against the reference's index_select of
+    every layer."""
+    import torch
+    from transformers import DynamicCache
+    from cast_amd.verify import cache_layers, gather_cache
+    n_prefix, n_pack, Hkv, D = 4096, 128, 8, 128
+    g = torch.Generator(device=dev).manual_seed(5)
+    full = [tuple(torch.randn((1, Hkv, n_prefix + n_pack, D), generator=g, device=dev).to(torch.bfloat16)
+                  for _ in range(2)) for _ in range(layers)]
+    cache = DynamicCache()
+    for i, (k, v) in enumerate(full):
+        cache.update(k, v, i)
+    n_layers, get, put = cache_layers(cache)
+    keep = [0, 1, 5, 9, 20, 33]
+
+    def restore():
+        for i, (k, v) in enumerate(full):
+            put(i, k, v)
+
+    def device():
+        restore()
+        gather_cache(cache, n_prefix, keep)
+
+    def reference_flow():
+        restore()
+        sel = torch.cat([torch.arange(n_prefix, device=dev), torch.tensor([n_prefix + i for i in keep], device=dev)])
+        for i in range(n_layers):
+            k, v = get(i)
+            put(i, k.index_select(2, sel), v.index_select(2, sel))
+
+    t_d = time_kernel(device, steps, warmup)
+    t_r = time_kernel(reference_flow, steps, warmup)
+    log(f"  gather_cache ({layers} layers, prefix {n_prefix}, keep {len(keep)}): in place {t_d:.1f} us, "
+        f"index_select {t_r:.1f} us")
+    return dict(in_place_us=round(t_d, 2), index_select_us=round(t_r, 2), layers=layers, prefix=n_prefix,
+                kept=len(keep))
+
+
 def draft_trees(dev, steps, warmup):
     """Drafting at Qwen3-8B shapes: B=8 requests x 15 future positions x the
     151936-entry vocabulary (bf16 logits), top-8 per position, one best-first
@@ -300,6 +342,7 @@ def secondary(dev, steps, warmup):
         torch.cuda.empty_cache()
     res["store_layout"] = store_layout(dev, steps, warmup)
     res["kv_append"] = kv_append(dev, steps, warmup)
+    res["cache_gather"] = cache_gather(dev, steps, warmup)
     res["draft_trees"] = draft_trees(dev, steps, warmup)
     # K1 and K3 on the headline trees, full Qwen3 vocabulary logits
     wl = scenarios.qwen3_headline()
@@ -326,7 +369,7 @@ def main():
     ap.add_argument("--kv-split", type=int, default=0, help="keys per split-K chunk (0: library choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=["kv_append", "draft_trees", "store_layout"],
+    ap.add_argument("--only", choices=["kv_append", "cache_gather", "draft_trees", "store_layout"],
                     help="only run one secondary workload (for kernel profiles); prints its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches), to scale HBM byte counters")
@@ -353,7 +396,8 @@ def main():
         print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
         return
     if args.only:
-        fn = {"kv_append": kv_append, "draft_trees": draft_trees, "store_layout": store_layout}[args.only]
+        fn = {"kv_append": kv_append, "cache_gather": cache_gather, "draft_trees": draft_trees,
+              "store_layout": store_layout}[args.only]
         print(json.dumps({args.only: fn(dev, args.steps, args.warmup)}), flush=True)
         return
     log(f"device: {torch.cuda.get_device_name(dev)}")

@@ -25,6 +25,8 @@ _LAZY = {
     "walk_tree": "verify",
     "walk_trees": "verify",
     "tree_attention_mask": "verify",
+    "cache_layers": "verify",
+    "gather_cache": "verify",
     "topk_marginals": "draft",
     "build_trees": "draft",
     "build_tree_device": "draft",

@@ -8,8 +8,15 @@
 // layer (serving.py:62, [Hkv, total_q, D]) to store slots
 // store_len[b] .. store_len[b] + len(path) of buf[layer][b] ([B, Hkv, cap, D]).
 // The reference issues two advanced-indexing copies per layer; here one
-// workgroup per (request, layer) moves 16-byte chunks, driven by the
+// workgroup per (request, layer, KV head) moves 16-byte chunks, driven by the
 // greedy-accept kernel's device-side path / path_len (no host round trip).
+//
+// Every workgroup loads all of its rows before it stores any (registers,
+// then a barrier), so the copy is also correct in place: pack and store may
+// be the same tensor, as in the batch-one cache compaction of
+// cast_trees/verify.py:48-60 (gather_cache), where row n_prefix + keep[j]
+// moves to n_prefix + j.  Different (request, layer, head) triples never
+// share an address.
 #include "cast_common.hpp"
 
 namespace cast {
@@ -31,42 +38,60 @@ struct AppendArgs {
     int32_t *status;
 };
 
-__global__ __launch_bounds__(256) void store_append_kernel(AppendArgs a) {
-    const int b = blockIdx.x, layer = blockIdx.y;
+constexpr int kAppendThreads = 256;
+constexpr int kAppendMaxChunks = 32;   // 16-byte chunks per (row, head): head_dim * esz <= 512 B
+constexpr int kAppendPerThread = kMaxPack * kAppendMaxChunks / kAppendThreads;
+
+__global__ __launch_bounds__(kAppendThreads) void store_append_kernel(AppendArgs a) {
+    const int b = blockIdx.x, layer = blockIdx.y, h = blockIdx.z;
     const int n = a.path_len[b];
     const int s0 = a.store_len[b];
     const int root = a.src_row[b];
     const int count = n + 1;     // root + accepted nodes
     if (n < 0 || n >= kMaxPack || s0 < 0 || s0 + count > a.cap || root < 0 || root >= a.total_q) {
-        if (threadIdx.x == 0 && layer == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        if (threadIdx.x == 0 && layer == 0 && h == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         return;
     }
-    if (threadIdx.x == 0 && layer == 0 && a.new_len) a.new_len[b] = s0 + count;
-    const char *kp = static_cast<const char *>(a.k_pack[layer]);
-    const char *vp = static_cast<const char *>(a.v_pack[layer]);
-    char *ks = static_cast<char *>(a.k_store[layer]) + (int64_t)b * a.ks_batch;
-    char *vs = static_cast<char *>(a.v_store[layer]) + (int64_t)b * a.vs_batch;
-    const int per_row = a.Hkv * a.chunks;
-    for (int idx = threadIdx.x; idx < count * per_row; idx += blockDim.x) {
-        const int j = idx / per_row;
-        const int h = (idx / a.chunks) % a.Hkv;
-        const int c = idx % a.chunks;
-        // keep[j]: the root (pack index 0), then node path[j-1] at pack index path[j-1] + 1
-        int pk = 0;
-        if (j > 0) {
-            const int node = a.path[(int64_t)b * a.path_stride + j - 1];
-            pk = node + 1;
-            if (node < 0 || root + pk >= a.total_q) {
-                raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
-                continue;
+    if (threadIdx.x == 0 && layer == 0 && h == 0 && a.new_len) a.new_len[b] = s0 + count;
+    const char *kp = static_cast<const char *>(a.k_pack[layer]) + (int64_t)h * a.kp_head;
+    const char *vp = static_cast<const char *>(a.v_pack[layer]) + (int64_t)h * a.vp_head;
+    char *ks = static_cast<char *>(a.k_store[layer]) + (int64_t)b * a.ks_batch + (int64_t)h * a.ks_head;
+    char *vs = static_cast<char *>(a.v_store[layer]) + (int64_t)b * a.vs_batch + (int64_t)h * a.vs_head;
+    const int total = count * a.chunks;   // <= kMaxPack * kAppendMaxChunks
+    // phase 1: every row this workgroup moves, into registers
+    u32x4 kx[kAppendPerThread], vx[kAppendPerThread];
+    bool ok[kAppendPerThread];
+#pragma unroll
+    for (int u = 0; u < kAppendPerThread; ++u) {
+        const int idx = threadIdx.x + u * kAppendThreads;
+        ok[u] = false;
+        if (idx < total) {
+            const int j = idx / a.chunks, c = idx % a.chunks;
+            // keep[j]: the root (pack index 0), then node path[j-1] at pack index path[j-1] + 1
+            int pk = 0;
+            if (j > 0) pk = a.path[(int64_t)b * a.path_stride + j - 1] + 1;
+            if (pk >= 1 || j == 0) {
+                if (root + pk < a.total_q) {
+                    const int64_t src = (int64_t)(root + pk);
+                    kx[u] = *reinterpret_cast<const u32x4 *>(kp + src * a.kp_tok + c * 16);
+                    vx[u] = *reinterpret_cast<const u32x4 *>(vp + src * a.vp_tok + c * 16);
+                    ok[u] = true;
+                }
             }
+            if (!ok[u]) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         }
-        const int64_t src = (int64_t)(root + pk);
-        const int64_t dst = (int64_t)(s0 + j);
-        const u32x4 kx = *reinterpret_cast<const u32x4 *>(kp + src * a.kp_tok + h * a.kp_head + c * 16);
-        const u32x4 vx = *reinterpret_cast<const u32x4 *>(vp + src * a.vp_tok + h * a.vp_head + c * 16);
-        *reinterpret_cast<u32x4 *>(ks + h * a.ks_head + dst * a.ks_tok + c * 16) = kx;
-        *reinterpret_cast<u32x4 *>(vs + h * a.vs_head + dst * a.vs_tok + c * 16) = vx;
+    }
+    __syncthreads();
+    // phase 2: the stores
+#pragma unroll
+    for (int u = 0; u < kAppendPerThread; ++u) {
+        const int idx = threadIdx.x + u * kAppendThreads;
+        if (idx < total && ok[u]) {
+            const int j = idx / a.chunks, c = idx % a.chunks;
+            const int64_t dst = (int64_t)(s0 + j);
+            *reinterpret_cast<u32x4 *>(ks + dst * a.ks_tok + c * 16) = kx[u];
+            *reinterpret_cast<u32x4 *>(vs + dst * a.vs_tok + c * 16) = vx[u];
+        }
     }
 }
 
@@ -90,7 +115,7 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     if (!k_pack || !v_pack || !k_store || !v_store || !src_row || !path || !path_len || !store_len)
         return CAST_ERR_NULL_POINTER;
     const int64_t esz = dtype == CAST_BF16 ? 2 : 4;
-    if ((head_dim * esz) % 16) return CAST_ERR_HEAD_DIM;
+    if ((head_dim * esz) % 16 || head_dim * esz > 16 * kAppendMaxChunks) return CAST_ERR_HEAD_DIM;
     const int64_t strides[10] = {kp_tok, kp_head, vp_tok, vp_head, ks_batch, ks_head, ks_tok, vs_batch, vs_head, vs_tok};
     for (int64_t s : strides)
         if ((s * esz) % 16) return CAST_ERR_ALIGNMENT;
@@ -122,6 +147,7 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     a.vs_head = vs_head * esz;
     a.vs_tok = vs_tok * esz;
     a.status = status;
-    store_append_kernel<<<dim3(batch, layers), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
+    store_append_kernel<<<dim3(batch, layers, num_kv_heads), kAppendThreads, 0,
+                          reinterpret_cast<hipStream_t>(stream)>>>(a);
     return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
 }

@@ -10,6 +10,11 @@
                       one device pass and one copy back
   tree_attention_mask the dense additive mask of cast_trees/verify.py:15-25
                       (host side; the batch-one decoder's mask semantics)
+  cache_layers        (n_layers, get, put) over a transformers DynamicCache
+                      (cast_trees/verify.py:28-45)
+  gather_cache        drop-in for cast_trees/verify.py:48-60: the accepted
+                      rows move in place on the device, all layers in one
+                      launch (K4), and the layers are cut to the kept length
 """
 from __future__ import annotations
 
@@ -132,3 +137,93 @@ def tree_attention_mask(n_prefix, nodes, device, dtype):
     mask = torch.zeros((1, 1, n, n_prefix + n), dtype=dtype)
     mask[0, 0, :, n_prefix:].masked_fill_(~vis, torch.finfo(dtype).min)
     return mask.to(device)
+
+
+def cache_layers(cache):
+    """(n_layers, get, put) over a DynamicCache: the per-layer objects of
+    recent transformers (``cache.layers[i].keys``) or the older
+    ``key_cache`` / ``value_cache`` lists."""
+    layers = getattr(cache, "layers", None)
+    if layers and hasattr(layers[0], "keys"):
+        def get(i):
+            return layers[i].keys, layers[i].values
+
+        def put(i, k, v):
+            layers[i].keys, layers[i].values = k, v
+        return len(layers), get, put
+
+    def get(i):
+        return cache.key_cache[i], cache.value_cache[i]
+
+    def put(i, k, v):
+        cache.key_cache[i], cache.value_cache[i] = k, v
+    return len(cache.key_cache), get, put
+
+
+def gather_cache(cache, n_prefix, keep):
+    """Keep the first ``n_prefix`` cached positions and then the packed
+    entries ``keep`` (``[0] + [i + 1 for i in path]``, as the decoder builds
+    it), in order, in every layer of a batch-one cache.
+
+    The kept rows n_prefix + keep[j] move to n_prefix + j in place, K and V
+    of all layers in one cast_store_append launch (each workgroup reads its
+    rows before it writes any, so the overlap is safe), and every layer
+    becomes a view of length n_prefix + len(keep).  The reference's
+    index_select copies every layer whole.
+    """
+    from .tree_attn import _DTYPES
+    n_layers, get, put = cache_layers(cache)
+    keep = [int(x) for x in keep]
+    if n_layers == 0:
+        return cache
+    layers = [get(i) for i in range(n_layers)]
+    k0 = layers[0][0]
+    if k0.dim() != 4 or k0.shape[0] != 1:
+        raise ValueError("gather_cache: a batch-one cache of [1, heads, seq, head_dim] layers")
+    _, Hkv, T, D = k0.shape
+    n = len(keep)
+    n_pack = T - n_prefix
+    if n and (keep[0] != 0 or n > min(MAX_PACK, n_pack) or min(keep[1:], default=1) < 1 or max(keep) >= n_pack):
+        raise ValueError(f"keep must be [0] + pack indices in [1, {n_pack}) with at most {MAX_PACK} entries")
+    if n_prefix < 0 or n_pack < 0:
+        raise ValueError("n_prefix beyond the cached length")
+    if n > 1:
+        shape, stride = k0.shape, k0.stride()
+        for k, v in layers:
+            if k.shape != shape or v.shape != shape or k.stride() != stride or v.stride() != stride \
+                    or k.dtype != k0.dtype or v.dtype != k0.dtype or k.device != k0.device or v.device != k0.device:
+                raise ValueError("gather_cache: every layer's K and V must share shape, strides, dtype and device")
+        if stride[3] != 1 or (stride[2] * k0.element_size()) % 16:
+            raise ValueError("gather_cache: contiguous head_dim rows, 16-byte aligned")
+        lib = _lib.load()
+        step = n_prefix * stride[2] * k0.element_size()   # the pack starts at row n_prefix
+        addrs = [k.data_ptr() for k, _ in layers] + [v.data_ptr() for _, v in layers]
+        if any(a % 16 for a in addrs):
+            raise ValueError("gather_cache: 16-byte aligned layers")
+        L = n_layers
+        # one host-to-device copy: [pack K | pack V | store K | store V] addresses, then
+        # int32 src_row, path_len, store_len, new_len and the [1, MAX_PACK] path
+        host = np.zeros(4 * L + (4 + MAX_PACK + 1) // 2, dtype=np.int64)
+        host[:L] = [a + step for a in addrs[:L]]
+        host[L:2 * L] = [a + step for a in addrs[L:]]
+        host[2 * L:4 * L] = addrs
+        i32 = host[4 * L:].view(np.int32)
+        i32[:4] = (0, n - 1, n_prefix, 0)
+        i32[4:4 + MAX_PACK] = -1
+        i32[4:4 + n - 1] = [x - 1 for x in keep[1:]]
+        dev_buf = torch.from_numpy(host).to(k0.device)
+        d32 = dev_buf[4 * L:].view(torch.int32)
+        ptrs = dev_buf[:4 * L]
+        with torch.cuda.device(k0.device):
+            st = lib.cast_store_append(
+                _lib.ptr(ptrs[:L]), _lib.ptr(ptrs[L:2 * L]), _lib.ptr(ptrs[2 * L:3 * L]),
+                _lib.ptr(ptrs[3 * L:]), L, _lib.ptr(d32[0:1]), _lib.ptr(d32[4:]), MAX_PACK,
+                _lib.ptr(d32[1:2]), _lib.ptr(d32[2:3]), _lib.ptr(d32[3:4]), 1, n_pack, T, Hkv, D,
+                stride[2], stride[1], stride[2], stride[1], stride[0], stride[1], stride[2],
+                stride[0], stride[1], stride[2], _DTYPES[k0.dtype], None, _lib.stream_of(k0))
+        _lib.check(st, "cast_store_append")
+    for i, (k, v) in enumerate(layers):
+        put(i, k[:, :, :n_prefix + n], v[:, :, :n_prefix + n])
+    if hasattr(cache, "_seen_tokens"):
+        cache._seen_tokens = n_prefix + n
+    return cache

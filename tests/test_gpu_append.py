@@ -122,3 +122,68 @@ def test_append_overflow_is_flagged(gpu):
     print("case append-overflow", flush=True)
     with pytest.raises(ValueError, match="inconsistent"):
         serving.append_accepted(buf_k, buf_v, [cap - 1, 0], cu_q, path, plen, pack_k, pack_v, check=True)
+
+
+def _reference_gather(layers, n_prefix, keep):
+    # cast_trees/verify.py:48-60: index_select of the prefix and the kept entries
+    dev = layers[0][0].device
+    sel = torch.arange(n_prefix, device=dev)
+    if keep:
+        sel = torch.cat([sel, torch.tensor([n_prefix + i for i in keep], device=dev)])
+    return [(k.index_select(2, sel), v.index_select(2, sel)) for k, v in layers]
+
+
+@pytest.mark.parametrize("case", ["path", "shift-by-one", "identity", "permuted", "root-only", "empty-prefix",
+                                  "fp32-d64", "old-layout"])
+def test_gather_cache_matches_reference(gpu, case):
+    # the batch-one compaction in place (rows overlap their sources) against index_select
+    from transformers import DynamicCache
+    from cast_amd.verify import cache_layers, gather_cache
+    rng = np.random.default_rng(sum(map(ord, case)))
+    dtype, D = (torch.float32, 64) if case == "fp32-d64" else (torch.bfloat16, 128)
+    L, Hkv, n_pack = 5, 4, 40
+    n_prefix = 0 if case == "empty-prefix" else 77
+    g = torch.Generator(device=gpu).manual_seed(7)
+    layers = [(torch.randn((1, Hkv, n_prefix + n_pack, D), generator=g, device=gpu).to(dtype),
+               torch.randn((1, Hkv, n_prefix + n_pack, D), generator=g, device=gpu).to(dtype)) for _ in range(L)]
+    if case == "shift-by-one":
+        keep = [0] + list(range(2, 30))
+    elif case == "identity":
+        keep = list(range(0, 25))
+    elif case == "permuted":
+        keep = [0] + rng.permutation(np.arange(1, n_pack))[:20].tolist()
+    elif case == "root-only":
+        keep = [0]
+    else:
+        keep = [0] + sorted(rng.choice(np.arange(1, n_pack), size=12, replace=False).tolist())
+    want = _reference_gather(layers, n_prefix, keep)
+    if case == "old-layout":
+        class _OldCache:
+            pass
+        cache = _OldCache()
+        cache.key_cache = [k.clone() for k, _ in layers]
+        cache.value_cache = [v.clone() for _, v in layers]
+    else:
+        cache = DynamicCache()
+        for i, (k, v) in enumerate(layers):
+            cache.update(k.clone(), v.clone(), i)
+    print(f"case gather_cache {case} keep={len(keep)}", flush=True)
+    gather_cache(cache, n_prefix, keep)
+    n_layers, get, _ = cache_layers(cache)
+    assert n_layers == L
+    for i in range(L):
+        k, v = get(i)
+        assert k.shape[2] == n_prefix + len(keep)
+        assert torch.equal(k, want[i][0]) and torch.equal(v, want[i][1]), f"layer {i}"
+    if case not in ("old-layout",):
+        assert cache.get_seq_length() == n_prefix + len(keep)
+
+
+def test_gather_cache_rejects_bad_keep(gpu):
+    from transformers import DynamicCache
+    from cast_amd.verify import gather_cache
+    cache = DynamicCache()
+    cache.update(torch.zeros((1, 2, 20, 64), device=gpu), torch.zeros((1, 2, 20, 64), device=gpu), 0)
+    for keep in ([1, 2], [0, 0], [0, 15]):
+        with pytest.raises(ValueError):
+            gather_cache(cache, 10, keep)
