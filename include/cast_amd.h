@@ -213,7 +213,11 @@ int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t vocab, int
  * Request b keeps its root and its accepted nodes (keep = [0] + [i + 1 for
  * i in path], cast_trees/serving.py:328-330) at slots store_len[b] .. in
  * order.  A request that would pass `cap` is skipped and flagged
- * CAST_FLAG_BAD_OFFSETS.
+ * CAST_FLAG_BAD_OFFSETS.  head_dim * element size <= 512 bytes.
+ * Pack and store may be the same memory (each (request, layer, head) is
+ * read whole before it is written): this is also the batch-one in-place
+ * compaction of cast_trees/verify.py:48-60 (gather_cache), with the pack
+ * at row n_prefix of the cache, store_len = n_prefix and batch = 1.
  * ------------------------------------------------------------------- */
 int cast_store_append(const void *const *k_pack, const void *const *v_pack, void *const *k_store,
                       void *const *v_store, int32_t layers, const int32_t *src_row,
