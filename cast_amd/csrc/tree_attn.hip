@@ -36,6 +36,7 @@ constexpr int kNoSplit = 1 << 30;        // chunk value meaning "one split"
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kRescaleSlack = 8.0f;    // log2 headroom before the O rescale
+constexpr int kCombineFast = 4;          // splits the combine loads in one round trip
 
 // Where the keys and values of request b, KV head h live.  Two layouts:
 //  concat (store == 0): one ragged [total_kv, Hkv, D] tensor per K and V;
@@ -639,25 +640,10 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     if (sq.part_off + (int64_t)sq.ns * sq.P > a.part_rows) return;
     const int64_t lstride = (int64_t)sq.P * a.Hq, xstride = lstride * D;
     const int hend = min(a.Hq, h0 + hpg);
-    for (int c = threadIdx.x; c < (hend - h0) * C; c += 256) {
+    const int ns = sq.ns;
+    auto finish = [&](int c, floatx4 acc, float M, float L) {
         const int hq = h0 + c / C, d4 = c % C;
-        const float *lp = a.part_lse + (sq.part_off + i) * a.Hq + hq;   // split s at + s*lstride
-        const float *xp = a.part_o + ((sq.part_off + i) * a.Hq + hq) * D + d4 * 4;
-        float M = -INFINITY;
-#pragma unroll 4
-        for (int s = 0; s < sq.ns; ++s) M = fmaxf(M, lp[s * lstride]);
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        float L = 0.f;
-        if (M != -INFINITY) {
-#pragma unroll 4
-            for (int s = 0; s < sq.ns; ++s) {
-                const float w = exp2f(lp[s * lstride] - M);
-                L += w;
-                const floatx4 x = *reinterpret_cast<const floatx4 *>(xp + s * xstride);
-                acc += w * x;
-            }
-            acc *= 1.f / L;
-        }
+        if (M != -INFINITY) acc *= 1.f / L;
         OutT *op = static_cast<OutT *>(a.out) + (int64_t)tok * a.o_tok + (int64_t)hq * a.o_head + d4 * 4;
         if constexpr (sizeof(OutT) == 2) {
             const u32x2 w = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
@@ -667,6 +653,67 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
         }
         if (a.lse && d4 == 0)
             a.lse[(int64_t)tok * a.Hq + hq] = M == -INFINITY ? -INFINITY : (M + log2f(L)) * kLn2;
+    };
+    const int nc = (hend - h0) * C;
+    if (ns <= kCombineFast) {
+        // up to kCombineFast splits: every split's LSE and partial of two
+        // chunks are loaded before any is used (one round trip)
+        for (int c0 = threadIdx.x; c0 < nc; c0 += 2 * 256) {
+            float lv[2][kCombineFast];
+            floatx4 xv[2][kCombineFast];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int c = min(c0 + u * 256, nc - 1);
+                const int hq = h0 + c / C, d4 = c % C;
+                const float *lp = a.part_lse + (sq.part_off + i) * a.Hq + hq;
+                const float *xp = a.part_o + ((sq.part_off + i) * a.Hq + hq) * D + d4 * 4;
+#pragma unroll
+                for (int s = 0; s < kCombineFast; ++s) {
+                    lv[u][s] = s < ns ? lp[s * lstride] : -INFINITY;
+                    xv[u][s] = s < ns ? *reinterpret_cast<const floatx4 *>(xp + s * xstride) : floatx4{};
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int c = c0 + u * 256;
+                if (c >= nc) break;
+                float M = -INFINITY;
+#pragma unroll
+                for (int s = 0; s < kCombineFast; ++s) M = fmaxf(M, lv[u][s]);
+                floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+                float L = 0.f;
+                if (M != -INFINITY) {
+#pragma unroll
+                    for (int s = 0; s < kCombineFast; ++s) {
+                        const float w = s < ns ? exp2f(lv[u][s] - M) : 0.f;
+                        L += w;
+                        acc += w * xv[u][s];
+                    }
+                }
+                finish(c, acc, M, L);
+            }
+        }
+        return;
+    }
+    for (int c = threadIdx.x; c < nc; c += 256) {
+        const int hq = h0 + c / C, d4 = c % C;
+        const float *lp = a.part_lse + (sq.part_off + i) * a.Hq + hq;   // split s at + s*lstride
+        const float *xp = a.part_o + ((sq.part_off + i) * a.Hq + hq) * D + d4 * 4;
+        float M = -INFINITY;
+#pragma unroll 4
+        for (int s = 0; s < ns; ++s) M = fmaxf(M, lp[s * lstride]);
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll 4
+            for (int s = 0; s < ns; ++s) {
+                const float w = exp2f(lp[s * lstride] - M);
+                L += w;
+                const floatx4 x = *reinterpret_cast<const floatx4 *>(xp + s * xstride);
+                acc += w * x;
+            }
+        }
+        finish(c, acc, M, L);
     }
 }
 
