@@ -132,7 +132,7 @@ def cpu_baseline(wl, budget_s=12.0):
 
     run()
     times, t_end = [], time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 30):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 150):   # ~12 s of CPU work
         t = time.perf_counter()
         run()
         times.append(time.perf_counter() - t)
