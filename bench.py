@@ -138,7 +138,13 @@ def cpu_baseline(wl, budget_s=12.0):
         times.append(time.perf_counter() - t)
     med = statistics.median(times)
     S0, P0 = int(wl.prefix_len[0]), int(wl.pack_len[0])
-    return dict(value=round(med * wl.B * 1e6, 1), unit="us/call", cores=cores, kind="port",
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return dict(value=round(med * wl.B * 1e6, 1), unit="us/call", cores=cores, kind="port", cpu=model,
                 sample=f"request 0 of {wl.B} (S={S0}, P={P0}, {wl.Hq}/{wl.Hkv} heads, D={wl.D}): dense fp32 "
                        f"torch oracle on the bf16-rounded inputs, median of {len(times)} runs "
                        f"({med * 1e3:.1f} ms each), scaled x{wl.B}")
