@@ -235,15 +235,24 @@ int cast_store_append(const void *const *k_pack, const void *const *v_pack, void
  *   logits   [rows, vocab] bf16 / fp32, row stride logits_ld elements
  *   top_idx  int64 [rows][k] token ids, top_lp  float [rows][k] log-probs,
  *            ranked by descending log-probability, equal values in
- *            increasing index order (cast_trees/tree.py:20-26); 1 <= k <= 16;
- *            finite logits
+ *            increasing index order (cast_trees/tree.py:20-26); 1 <= k <= 16,
+ *            k <= vocab.  -inf logits rank by index like any value; NaN
+ *            logits never rank (a row with fewer than k non-NaN entries gets
+ *            index -1 and a NaN log-prob in its last slots), and a NaN or
+ *            +inf anywhere in a row makes its log-probs NaN, as log_softmax
+ *            does.
  * cast_build_trees replaces build_tree (cast_trees/tree.py:29-49), one tree
  * per request, the same heap order (-score, depth, parent, rank, counter):
  *   top_idx / top_lp  [batch][L][k] as written by cast_draft_topk; top_lp
  *            float (lp_dtype CAST_FP32) or double (CAST_FP64)
- *   budget   int32 [batch] non-root nodes wanted (<= 127)
+ *   budget   int32 [batch] non-root nodes wanted (<= 127; larger values
+ *            are clamped and flag CAST_FLAG_BAD_PACK in *status)
  *   token int64, depth int32, parent int32 (node index, -1 = root child),
  *   score double: [batch][127] nodes in pop order;  n_nodes int32 [batch]
+ *   1 <= L <= 255, 1 <= k <= 16.  Log-probs must not be NaN or +inf (the
+ *   reference's heap has no defined order then).  Positions whose log-probs
+ *   are non-increasing in rank (top-k output) take a sorted-frontier search;
+ *   others a scan of every pushed candidate; both pop the heap's order.
  * ------------------------------------------------------------------- */
 int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t rows, int32_t vocab,
                     int32_t dtype, int32_t k, int64_t *top_idx, float *top_lp,
