@@ -59,8 +59,14 @@ def build_trees(top_idx, top_lp, budget, k=None, *, check=False):
     lib = _lib.load()
     if top_idx.dim() == 2:
         top_idx, top_lp = top_idx[None], top_lp[None]
+    if top_idx.dim() != 3 or top_lp.shape != top_idx.shape:
+        raise ValueError("top_idx and top_lp must both be [B, L, k] (or [L, k])")
+    if not (top_idx.is_cuda and top_lp.is_cuda) or top_lp.device != top_idx.device:
+        raise ValueError("top_idx and top_lp must be on one GPU")
     B, L, kk = top_idx.shape
     k = kk if k is None else min(int(k), kk)
+    if L < 1 or L > 255 or k < 1 or k > 16:
+        raise ValueError("build_trees needs 1 <= L <= 255 future positions and 1 <= k <= 16 candidates")
     dev = top_idx.device
     ti = top_idx[..., :k].to(torch.int64).contiguous()
     tl = top_lp[..., :k]
@@ -70,6 +76,8 @@ def build_trees(top_idx, top_lp, budget, k=None, *, check=False):
     if isinstance(budget, int):
         budget = torch.full((B,), budget, dtype=torch.int32, device=dev)
     budget = torch.as_tensor(budget, device=dev).to(torch.int32).contiguous()
+    if budget.shape != (B,):
+        raise ValueError(f"budget must be an int or [{B}] per-request node counts")
     n = MAX_PACK - 1
     token = torch.empty((B, n), dtype=torch.int64, device=dev)
     depth = torch.empty((B, n), dtype=torch.int32, device=dev)

@@ -137,3 +137,14 @@ def test_append_layout_checked_once_and_rechecked_on_change():
     buf_k[2] = torch.empty((2, 2, 16, 64), dtype=torch.bfloat16)
     again = serving._append_layout(buf_k, buf_v, pack_k, pack_v)
     assert again is not first and again["ptrs"][L * 2 + 2].item() == buf_k[2].data_ptr()
+
+
+def test_build_trees_checks_inputs_before_launch():
+    # shape mismatches and host tensors are refused before any device work
+    import torch
+    from cast_amd.draft import build_trees
+    ti = torch.zeros((2, 15, 8), dtype=torch.int64)
+    with pytest.raises(ValueError, match="both be"):
+        build_trees(ti, torch.zeros((2, 15, 4)), 15)
+    with pytest.raises(ValueError, match="one GPU"):
+        build_trees(ti, torch.zeros((2, 15, 8)), 15)
