@@ -62,6 +62,8 @@ def greedy_accept(logits, cu_q, parent, token, *, check=False):
     [B]; bonus int64 [B]; argmax int32 [total_q]).
     """
     lib = _lib.load()
+    if not logits.is_cuda:
+        raise ValueError("greedy_accept runs on the GPU: logits must be a device tensor")
     dev = logits.device
     if logits.dtype not in (torch.bfloat16, torch.float32):
         logits = logits.float()

@@ -148,3 +148,10 @@ def test_build_trees_checks_inputs_before_launch():
         build_trees(ti, torch.zeros((2, 15, 4)), 15)
     with pytest.raises(ValueError, match="one GPU"):
         build_trees(ti, torch.zeros((2, 15, 8)), 15)
+
+
+def test_greedy_accept_refuses_host_logits():
+    import torch
+    from cast_amd.verify import greedy_accept
+    with pytest.raises(ValueError, match="device tensor"):
+        greedy_accept(torch.zeros((3, 10)), [0, 3], [-1, 0, 0], [0, 1, 2])
