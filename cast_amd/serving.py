@@ -207,6 +207,13 @@ def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_
     lib = _lib.load()
     lay = _append_layout(buf_k, buf_v, pack_k, pack_v)
     L, B = lay["L"], lay["B"]
+    dev = lay["device"]
+    if dev.type != "cuda":
+        raise ValueError("the KV append runs on the GPU: stores and packs must be device tensors")
+    for name, t in (("src_row", src_row), ("path", path), ("path_len", path_len), ("store_len", store_len),
+                    ("new_len", new_len), ("status", status)):
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} must be on the stores' device {dev}")
     n = int(src_row.shape[0])
     if n > B or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
         raise ValueError("path must be [B, >=128] (as written by greedy_accept) for B <= the store batch")
@@ -236,8 +243,8 @@ def append_accepted(buf_k, buf_v, store_len, cu_q, path, path_len, pack_k=None, 
     cu_q = torch.as_tensor(cu_q, device=dev).to(torch.int32).contiguous()
     new_len = torch.empty_like(store_len)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
-    _append_launch(buf_k, buf_v, pack_k, pack_v, cu_q[:-1].contiguous(), path.to(torch.int32),
-                   path_len.to(torch.int32).contiguous(), store_len, new_len, status)
+    _append_launch(buf_k, buf_v, pack_k, pack_v, cu_q[:-1].contiguous(), path.to(dev, torch.int32),
+                   path_len.to(dev, torch.int32).contiguous(), store_len, new_len, status)
     if check:
         from . import _lib
         _lib.raise_device_flags(status.item(), "append_accepted")

@@ -57,6 +57,14 @@ def _mask_words(mask, total_q, device):
     return m.contiguous(), words
 
 
+def _require_on(dev, **tensors):
+    """Every given tensor (None skipped) on q's device: the kernels take raw
+    device pointers, so a host or other-GPU tensor is refused here."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q on {dev}: all tensors must be on one GPU")
+
+
 def _ready(x, esz):
     """Last dim contiguous, 16-byte aligned base and strides."""
     if x.stride(-1) != 1 or x.data_ptr() % 16 or any((s * esz) % 16 for s in x.stride()[:-1]):
@@ -105,6 +113,7 @@ def varlen_tree_attention(q, k, v, cu_q, cu_kv, prefix_len, pack_len, ancestor_m
         raise ValueError("k and v must both be [total_kv, H_kv, D] with the head dim of q")
     esz = q.element_size()
     dev = q.device
+    _require_on(dev, k=k, v=v, out=out, workspace=workspace)
     q, k, v = _ready(q, esz), _ready(k, esz), _ready(v, esz)
     cu_q = _as_i32(cu_q, dev)
     cu_kv = _as_i32(cu_kv, dev)
@@ -184,6 +193,7 @@ def store_tree_attention(q, k_store, v_store, k_pack, v_pack, cu_q, prefix_len, 
         sm_scale = 1.0 / math.sqrt(D)
     esz = q.element_size()
     dev = q.device
+    _require_on(dev, k_store=k_store, v_store=v_store, k_pack=k_pack, v_pack=v_pack, out=out, workspace=workspace)
     q, k_pack, v_pack = _ready(q, esz), _ready(k_pack, esz), _ready(v_pack, esz)
     if _ready(k_store, esz) is not k_store or _ready(v_store, esz) is not v_store:
         raise ValueError("the store needs a contiguous head dim and 16-byte aligned strides")

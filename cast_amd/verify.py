@@ -182,6 +182,8 @@ def gather_cache(cache, n_prefix, keep):
     k0 = layers[0][0]
     if k0.dim() != 4 or k0.shape[0] != 1:
         raise ValueError("gather_cache: a batch-one cache of [1, heads, seq, head_dim] layers")
+    if not k0.is_cuda:
+        raise ValueError("gather_cache runs on the GPU: the cache must hold device tensors")
     _, Hkv, T, D = k0.shape
     n = len(keep)
     n_pack = T - n_prefix

@@ -155,3 +155,16 @@ def test_greedy_accept_refuses_host_logits():
     from cast_amd.verify import greedy_accept
     with pytest.raises(ValueError, match="device tensor"):
         greedy_accept(torch.zeros((3, 10)), [0, 3], [-1, 0, 0], [0, 1, 2])
+
+
+def test_attention_wrappers_refuse_tensors_on_other_devices():
+    # q on the "device" check passes only for CUDA tensors; a host K next to a
+    # device q would hand host pointers to the kernel, so it is refused first
+    import torch
+    from cast_amd import tree_attn
+    q = torch.zeros((4, 8, 64))
+    with pytest.raises(ValueError, match="on the GPU|device"):
+        tree_attn.varlen_tree_attention(q, torch.zeros((9, 2, 64)), torch.zeros((9, 2, 64)), [0, 4], [0, 9],
+                                        [5], [4], torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(ValueError, match="one GPU"):
+        tree_attn._require_on(torch.device("cuda", 0), k=torch.zeros(1))
