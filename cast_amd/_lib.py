@@ -44,7 +44,8 @@ SIGNATURES = {
     "cast_tree_attn_default_split": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32], _I32),
     "cast_store_append": ([_P] * 4 + [_I32] + [_P] * 2 + [_I32] + [_P] * 3 + [_I32] * 5 + [_I64] * 10 +
                           [_I32, _P, _P], ctypes.c_int),
-    "cast_draft_topk": ([_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
+    "cast_draft_topk": ([_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
+    "cast_draft_topk_workspace_size": ([_I32, _I32, _I32, _I32, _I32], _SZ),
     "cast_build_trees": ([_P, _P, _I32, _I32, _I32, _I32] + [_P] * 8, ctypes.c_int),
     "cast_greedy_accept": ([_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P], ctypes.c_int),
 }

@@ -76,27 +76,100 @@ __device__ __forceinline__ uint64_t row_key_max(uint64_t key) {
     return lane_key(key, 15);
 }
 
-// One workgroup per row: top-k (value, index) and the row's log-sum-exp.
+// Partial result of one (row, split) workgroup: its slice's top-k keys and
+// the slice's log-sum-exp as (max, sum of exp(x - max)).
+struct TopkPart {
+    uint64_t key[kTopKMax];   // descending, 0 = empty
+    double sum;
+    float mx;                 // -inf for a slice without elements
+    float pad;
+};
+constexpr int kTopkNT = 512;          // threads of a top-k workgroup
+constexpr int kTopkBatch = 8;         // 16-byte chunks per thread per batch
+constexpr int kTopkMaxSplits = 8;
+
+// Rank selection over candidates held in LDS: every candidate (unique keys,
+// 0 = none) counts the candidates above it, and a rank below k is its slot.
+// Threads 0..n-1 hold one candidate each (cand[tid]); slots stay as set.
+__device__ __forceinline__ void rank_select(const uint64_t *cand, int n, int k, uint64_t *slots) {
+    const int tid = threadIdx.x;
+    if (tid < n) {
+        const uint64_t mine = cand[tid];
+        int above = 0;
+        for (int j = 0; j < n; ++j) above += cand[j] > mine ? 1 : 0;
+        if (above < k && mine != 0) slots[above] = mine;
+    }
+}
+
+// One wave per row: the splits' top-k lists and log-sum-exp partials into
+// the row's top k and log probabilities (splits * k <= 64).  A kernel of its
+// own: the launch boundary makes every part visible, where a last-workgroup
+// ticket would need a device-scope release (an L2 write-back) per workgroup.
+__global__ __launch_bounds__(64) void draft_topk_combine_kernel(const TopkPart *__restrict__ part, int32_t splits,
+                                                                int32_t k, int64_t *__restrict__ top_idx,
+                                                                float *__restrict__ top_lp) {
+    __shared__ uint64_t cand[64];
+    __shared__ uint64_t slots[kTopKMax];
+    const int row = blockIdx.x, lane = threadIdx.x;
+    const TopkPart *pp = part + (size_t)row * splits;
+    top_idx += (size_t)row * k;
+    top_lp += (size_t)row * k;
+    const int n = splits * k;
+    if (lane < kTopKMax) slots[lane] = 0;
+    cand[lane] = lane < n ? pp[lane / k].key[lane % k] : 0;
+    const float m = lane < splits ? pp[lane].mx : -INFINITY;
+    float gm = m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+    double sum = lane < splits && m != -INFINITY ? pp[lane].sum * exp((double)m - (double)gm) : 0.0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    __syncthreads();
+    rank_select(cand, n, k, slots);
+    __syncthreads();
+    if (lane < k) {
+        const float log_sum = (float)log(sum);
+        const uint64_t key = slots[lane];
+        top_idx[lane] = key == 0 ? -1 : key_index(key);
+        top_lp[lane] = key == 0 ? NAN : (key_value(key) - gm) - log_sum;
+    }
+}
+
+// One workgroup per (row, split): top-k (value, index) and log-sum-exp of the
+// split's slice of the row, elements [split * per_e, +per_e) (per_e a
+// multiple of the 16-byte chunk).  With one split it writes the row's log
+// probabilities; with several it writes a TopkPart for the combine kernel.
 //
 // Each thread keeps its best K rank keys (K >= k) in a fully unrolled sorted
-// list; k merge rounds of the list heads give the row's top k.  Only
-// elements whose key is at least a threshold key enter the lists.  The
-// threshold comes from the first batch (4 chunks of 16 bytes per thread):
-// the k-th largest of the threads' best keys, a bound no final top-k element
-// falls below since k real elements are at or above it.  A chunk whose max
-// is below the threshold's value skips the per-element test.
+// list.  Only elements whose key is at least a threshold key enter the lists.
+// The threshold comes from the first batch (8 chunks per thread): the
+// smallest of the waves' best thread keys (the two best for k > 8), a bound
+// no final top-k element of the slice falls below since at least k distinct
+// elements are at or above it.  A chunk whose max is below the threshold's
+// value skips the per-element test.  The lists' entries are then compacted
+// into LDS and ranked by counting (k rounds over the list heads when more
+// than kTopkNT entries survive).
 //
-// Log-sum-exp: per 16-byte chunk, the chunk's max updates the thread's
-// running max, the chunk's exp terms are summed pairwise in float and the
-// thread's total is rescaled and accumulated in double.
+// Log-sum-exp: a running max per thread; a chunk's exp terms are summed
+// pairwise in float onto the thread's float sum, which is rescaled only when
+// the running max moves.  Workgroup and split sums are combined in double.
 template <bool BF16, int K>
-__global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict__ logits, int64_t ld, int32_t vocab,
-                                                         int32_t k, int64_t *__restrict__ top_idx,
-                                                         float *__restrict__ top_lp) {
-    constexpr int NT = 512, NW = NT / 64;
+__global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restrict__ logits, int64_t ld,
+                                                             int32_t vocab, int32_t k, int32_t per_e,
+                                                             TopkPart *__restrict__ part,
+                                                             int64_t *__restrict__ top_idx,
+                                                             float *__restrict__ top_lp) {
+    constexpr int NT = kTopkNT, NW = NT / 64, NB = kTopkBatch;
     constexpr float kLog2e = 1.4426950408889634f;
-    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    constexpr int EPC = BF16 ? 8 : 4;
+    const int row = blockIdx.x, split = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const char *base = static_cast<const char *>(logits) + (size_t)row * (size_t)ld * (BF16 ? 2 : 4);
+    const int e0 = split * per_e;
+    const int e1 = max(e0, min(vocab, e0 + per_e));   // an empty last split stays empty
+    const bool vec = (reinterpret_cast<uintptr_t>(base) & 15) == 0;
+    const int cb = vec ? e0 / EPC : 0, ce = vec ? e1 / EPC : 0;   // this split's whole chunks
+    const int tail0 = vec ? ce * EPC : e0;                         // then elements [tail0, e1)
+
     uint64_t tk[K];   // descending; 0 = empty
 #pragma unroll
     for (int j = 0; j < K; ++j) tk[j] = 0;
@@ -119,44 +192,30 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
             }
         }
     };
-    float mx = -INFINITY;   // running max; sum holds sum(exp(x - mx))
-    double sum = 0.0;
+    // running max mx; fsum holds sum(2^(x * log2e - ref2)) with ref2 the
+    // rounded mx * log2e (0 while mx = -inf) and eps2 = mx * log2e - ref2
+    // exactly, so fsum * 2^-eps2 = sum(exp(x - mx)).  One FMA per element
+    // (the product is exact inside it), however large the logits.
+    float mx = -INFINITY, ref2 = 0.f, eps2 = 0.f;
+    float fsum = 0.f;
     auto lse_add = [&](const auto &v, float m) __attribute__((always_inline)) {   // m = max(v)
         constexpr int n = sizeof(v) / sizeof(float);
-        const float nm = fmaxf(mx, m);
-        const float ref = nm == -INFINITY ? 0.f : nm;
+        if (m > mx) {   // a sum of -inf terms only is 0 (a NaN sum stays NaN)
+            const float r = m * kLog2e;
+            fsum *= mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ref2 - r);
+            eps2 = fmaf(m, kLog2e, -r);
+            ref2 = r;
+            mx = m;
+        }
         float ex[n];
 #pragma unroll
-        for (int e = 0; e < n; ++e) ex[e] = __builtin_amdgcn_exp2f((v[e] - ref) * kLog2e);
+        for (int e = 0; e < n; ++e) ex[e] = __builtin_amdgcn_exp2f(fmaf(v[e], kLog2e, -ref2));
 #pragma unroll
         for (int w = 1; w < n; w *= 2)   // pairwise
 #pragma unroll
             for (int e = 0; e + w < n; e += 2 * w) ex[e] += ex[e + w];
-        sum = sum * (double)__builtin_amdgcn_exp2f((mx - ref) * kLog2e) + (double)ex[0];
-        mx = nm;
+        fsum += ex[0];
     };
-    // k rounds over the list heads: the k largest keys of all lists, in
-    // order, into topk (the popped heads leave their lists); one barrier per
-    // round, the per-wave maxima double-buffered by round parity
-    __shared__ uint64_t wmax[2][NW], topk[K];
-    auto merge = [&]() __attribute__((always_inline)) {
-        for (int r = 0; r < k; ++r) {
-            uint64_t best = wave_key_max(tk[0]);
-            if (lane == 0) wmax[r & 1][wv] = best;
-            __syncthreads();
-            best = row_key_max(lane < NW ? wmax[r & 1][lane] : 0);
-            if (tk[0] == best && best != 0) {   // keys are unique: one owner pops
-#pragma unroll
-                for (int j = 0; j < K - 1; ++j) tk[j] = tk[j + 1];
-                tk[K - 1] = 0;
-            }
-            if (tid == 0) topk[r] = best;
-        }
-        __syncthreads();
-    };
-    constexpr int EPC = BF16 ? 8 : 4;
-    const bool vec = (reinterpret_cast<uintptr_t>(base) & 15) == 0;
-    const int nch = vec ? vocab / EPC : 0;
     auto unpack = [&](const u32x4 &w, float (&v)[EPC]) __attribute__((always_inline)) {
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
@@ -194,17 +253,22 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
         lse_add(v, m);
         filter(v, m, c);
     };
-    auto load4 = [&](u32x4 (&w)[4], int c0) __attribute__((always_inline)) {
+    auto load_batch = [&](u32x4 (&w)[NB], int c0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c0 + u * NT) * 16);
+        for (int u = 0; u < NB; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c0 + u * NT) * 16);
     };
-    int c = tid;
-    if (nch >= 4 * NT) {   // first batch: the threshold, then the batch through it
-        u32x4 w[4];
-        load4(w, c);
+
+    constexpr int R = K > 8 ? 2 : 1;   // best keys taken per wave for the threshold
+    __shared__ uint64_t thr_keys[NW * R];
+    int c = cb + tid;
+    u32x4 nxt[NB];
+    if (ce - cb >= NB * NT) {   // first batch: the threshold, then the batch through it
+        u32x4 w[NB];
+        load_batch(w, c);
+        if (c + NB * NT + (NB - 1) * NT < ce) load_batch(nxt, c + NB * NT);
         uint64_t best = 0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < NB; ++u) {
             float v[EPC];
             unpack(w[u], v);
             const float m = chunk_max(v);
@@ -215,43 +279,64 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
             const uint64_t key = rank_key(m, (c + u * NT) * EPC + fi);
             best = key > best ? key : best;
         }
-        tk[0] = best;
-        merge();
-        if (topk[k - 1] != 0) {
-            thr = topk[k - 1];
-            thr_v = key_value(thr);
-            thr_i = key_index(thr);
-        }
-        tk[0] = 0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int r = 0; r < R; ++r) {   // the wave's R best thread keys (unique keys: one owner)
+            const uint64_t wb = wave_key_max(best);
+            if (lane == 0) thr_keys[wv * R + r] = wb;
+            if (best == wb) best = 0;
+        }
+        __syncthreads();
+        uint64_t t = thr_keys[0];
+#pragma unroll
+        for (int i = 1; i < NW * R; ++i) t = thr_keys[i] < t ? thr_keys[i] : t;
+        if (t != 0) {   // NW * R >= k distinct real elements are at or above t
+            thr = t;
+            thr_v = key_value(t);
+            thr_i = key_index(t);
+        }
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
             float v[EPC];
             unpack(w[u], v);
             filter(v, chunk_max(v), c + u * NT);
         }
-        c += 4 * NT;
+        c += NB * NT;
+    } else if (c + (NB - 1) * NT < ce) {
+        load_batch(nxt, c);
     }
-    // the rest in batches of 4 chunks, the next batch loading while this one is consumed
-    u32x4 nxt[4];
-    if (c + 3 * NT < nch) load4(nxt, c);
-    for (; c + 3 * NT < nch; c += 4 * NT) {
-        u32x4 w[4];
+    // the rest in batches, the next batch loading while this one is consumed
+    for (; c + (NB - 1) * NT < ce; c += NB * NT) {
+        u32x4 w[NB];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = nxt[u];
-        if (c + 7 * NT < nch) load4(nxt, c + 4 * NT);
+        for (int u = 0; u < NB; ++u) w[u] = nxt[u];
+        if (c + NB * NT + (NB - 1) * NT < ce) load_batch(nxt, c + NB * NT);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) chunk(w[u], c + u * NT);
+        for (int u = 0; u < NB; ++u) chunk(w[u], c + u * NT);
     }
-    for (; c < nch; c += NT) chunk(*reinterpret_cast<const u32x4 *>(base + (size_t)c * 16), c);
-    for (int i = nch * EPC + tid; i < vocab; i += NT) {
+    {   // the remainder, fewer than NB chunks per thread, in one round trip
+        u32x4 w[NB];
+#pragma unroll
+        for (int u = 0; u < NB - 1; ++u)
+            if (c + u * NT < ce) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c + u * NT) * 16);
+#pragma unroll
+        for (int u = 0; u < NB - 1; ++u)
+            if (c + u * NT < ce) chunk(w[u], c + u * NT);
+    }
+    for (int i = tail0 + tid; i < e1; i += NT) {
         const float v[1] = {logit_at<BF16>(base, i)};
         lse_add(v, v[0]);
         const uint64_t key = rank_key(v[0], i);
         if (key >= thr) insert(key);
     }
-    // workgroup log-sum-exp: max, then the sums rescaled to it
+
+    // ---- the slice's log-sum-exp: max, then the sums rescaled to it
     __shared__ float red[NW];
     __shared__ double dred[NW];
+    __shared__ int n_cand;
+    __shared__ uint64_t cand[NT];
+    __shared__ uint64_t topk[kTopKMax];
+    if (tid == 0) n_cand = 0;
+    if (tid < kTopKMax) topk[tid] = 0;
     float gm = mx;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
@@ -260,17 +345,51 @@ __global__ __launch_bounds__(512) void draft_topk_kernel(const void *__restrict_
     gm = red[0];
 #pragma unroll
     for (int w = 1; w < NW; ++w) gm = fmaxf(gm, red[w]);
-    sum = mx == -INFINITY ? 0.0 : sum * exp((double)mx - (double)gm);
+    double sum = mx == -INFINITY ? 0.0 : (double)fsum * (double)__builtin_amdgcn_exp2f((mx - gm) * kLog2e - eps2);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
     if (lane == 0) dred[wv] = sum;
+
+    // ---- the slice's top k: the lists' entries compacted into LDS, ranked
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < K; ++j) mine += tk[j] != 0 ? 1 : 0;
+    const int at = mine ? atomicAdd(&n_cand, mine) : 0;
     __syncthreads();
+    const int n = n_cand;
     double tot = 0.0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) tot += dred[w];
-    const float log_sum = (float)log(tot);
-    merge();
-    if (tid < k) {
+    if (n <= NT) {
+#pragma unroll
+        for (int j = 0; j < K; ++j)
+            if (j < mine) cand[at + j] = tk[j];
+        __syncthreads();
+        rank_select(cand, n, k, topk);
+    } else {   // many survivors: k rounds over the list heads
+        for (int r = 0; r < k; ++r) {
+            uint64_t best = wave_key_max(tk[0]);
+            if (lane == 0) cand[(r & 1) * NW + wv] = best;
+            __syncthreads();
+            best = row_key_max(lane < NW ? cand[(r & 1) * NW + lane] : 0);
+            if (tk[0] == best && best != 0) {   // keys are unique: one owner pops
+#pragma unroll
+                for (int j = 0; j < K - 1; ++j) tk[j] = tk[j + 1];
+                tk[K - 1] = 0;
+            }
+            if (tid == 0) topk[r] = best;
+        }
+    }
+    __syncthreads();
+    if (part) {
+        TopkPart *pp = part + (size_t)row * gridDim.y + split;
+        if (tid < kTopKMax) pp->key[tid] = topk[tid];
+        if (tid == 0) {
+            pp->sum = tot;
+            pp->mx = gm;
+        }
+    } else if (tid < k) {
+        const float log_sum = (float)log(tot);
         const uint64_t key = topk[tid];
         top_idx[(size_t)row * k + tid] = key == 0 ? -1 : key_index(key);
         top_lp[(size_t)row * k + tid] = key == 0 ? NAN : (key_value(key) - gm) - log_sum;   // (x - max) - log(sum)
@@ -508,21 +627,58 @@ __global__ __launch_bounds__(64) void build_trees_kernel(const int64_t *__restri
 
 using namespace cast;
 
+// Splits per row: about one workgroup per CU (a workgroup's registers fill
+// most of a CU), each split at least one first batch long, and
+// splits * k <= 64 for the combine wave.
+static int topk_splits(int32_t rows, int32_t vocab, int32_t dtype, int32_t k, int32_t want) {
+    const int per_batch = kTopkBatch * kTopkNT * (dtype == CAST_BF16 ? 8 : 4);
+    int cap = vocab / per_batch;
+    cap = cap < 64 / k ? cap : 64 / k;
+    cap = cap < kTopkMaxSplits ? cap : kTopkMaxSplits;
+    if (cap < 1) cap = 1;
+    int s = want > 0 ? want : 256 / rows;
+    if (s < 1) s = 1;
+    return s < cap ? s : cap;
+}
+
+extern "C" size_t cast_draft_topk_workspace_size(int32_t rows, int32_t vocab, int32_t dtype, int32_t k,
+                                                 int32_t splits) {
+    if (rows <= 0 || vocab <= 0 || k < 1 || k > kTopKMax) return 0;
+    const int s = topk_splits(rows, vocab, dtype, k, splits);
+    return s > 1 ? (size_t)rows * s * sizeof(TopkPart) : 0;
+}
+
 extern "C" int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t rows, int32_t vocab, int32_t dtype,
-                               int32_t k, int64_t *top_idx, float *top_lp, cast_stream_t stream) {
-    if (rows < 0 || vocab <= 0 || logits_ld < vocab || k < 1 || k > kTopKMax || k > vocab) return CAST_ERR_SHAPE;
+                               int32_t k, int64_t *top_idx, float *top_lp, int32_t splits, void *workspace,
+                               size_t workspace_bytes, cast_stream_t stream) {
+    if (rows < 0 || vocab <= 0 || logits_ld < vocab || k < 1 || k > kTopKMax || k > vocab || splits < 0)
+        return CAST_ERR_SHAPE;
     if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
     if (rows == 0) return CAST_OK;
     if (!logits || !top_idx || !top_lp) return CAST_ERR_NULL_POINTER;
+    const int ns = topk_splits(rows, vocab, dtype, k, splits);
+    TopkPart *part = nullptr;
+    if (ns > 1) {
+        if (!workspace) return CAST_ERR_NULL_POINTER;
+        if (workspace_bytes < (size_t)rows * ns * sizeof(TopkPart)) return CAST_ERR_WORKSPACE;
+        if (reinterpret_cast<uintptr_t>(workspace) & 15) return CAST_ERR_ALIGNMENT;
+        part = static_cast<TopkPart *>(workspace);
+    }
+    const int epc = dtype == CAST_BF16 ? 8 : 4;
+    const int32_t per_e = (int32_t)(((int64_t)vocab + ns * epc - 1) / (ns * epc) * epc);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const dim3 grid(rows, ns);
     if (dtype == CAST_BF16 && k <= 8)
-        draft_topk_kernel<true, 8><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+        draft_topk_kernel<true, 8><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx, top_lp);
     else if (dtype == CAST_BF16)
-        draft_topk_kernel<true, kTopKMax><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+        draft_topk_kernel<true, kTopKMax><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx,
+                                                                   top_lp);
     else if (k <= 8)
-        draft_topk_kernel<false, 8><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+        draft_topk_kernel<false, 8><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx, top_lp);
     else
-        draft_topk_kernel<false, kTopKMax><<<rows, 512, 0, s>>>(logits, logits_ld, vocab, k, top_idx, top_lp);
+        draft_topk_kernel<false, kTopKMax><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx,
+                                                                    top_lp);
+    if (ns > 1) draft_topk_combine_kernel<<<rows, 64, 0, s>>>(part, ns, k, top_idx, top_lp);
     return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
 }
 

@@ -21,12 +21,14 @@ from . import _lib
 from .tree import MAX_PACK, TreeNode
 
 
-def topk_marginals(d_logits, k, *, on_device=False):
+def topk_marginals(d_logits, k, *, on_device=False, splits=0):
     """Top-k token ids and log-probs at each future position.
 
     d_logits: [L, V] (or [rows, V]) bf16/fp32 on the device.  Returns (indices
     int64 [L, k], values float32 [L, k]), moved to the host like the reference
-    unless ``on_device``.
+    unless ``on_device``.  ``splits`` sets the workgroups per row (0: chosen
+    from the shape); the results do not depend on it beyond float rounding
+    of the log-sum-exp.
     """
     lib = _lib.load()
     x = d_logits
@@ -37,11 +39,14 @@ def topk_marginals(d_logits, k, *, on_device=False):
     if x.stride(1) != 1:
         x = x.contiguous()
     rows, V = x.shape
+    dt = _lib.BF16 if x.dtype == torch.bfloat16 else _lib.FP32
     idx = torch.empty((rows, k), dtype=torch.int64, device=x.device)
     lp = torch.empty((rows, k), dtype=torch.float32, device=x.device)
+    ws_bytes = lib.cast_draft_topk_workspace_size(rows, V, dt, k, int(splits)) if 1 <= k <= 16 else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     with torch.cuda.device(x.device):
-        st = lib.cast_draft_topk(_lib.ptr(x), x.stride(0), rows, V, _lib.BF16 if x.dtype == torch.bfloat16 else _lib.FP32,
-                                 k, _lib.ptr(idx), _lib.ptr(lp), _lib.stream_of(x))
+        st = lib.cast_draft_topk(_lib.ptr(x), x.stride(0), rows, V, dt, k, _lib.ptr(idx), _lib.ptr(lp),
+                                 int(splits), _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
     _lib.check(st, "cast_draft_topk")
     return (idx, lp) if on_device else (idx.cpu(), lp.cpu())
 

@@ -241,6 +241,13 @@ int cast_store_append(const void *const *k_pack, const void *const *v_pack, void
  *            index -1 and a NaN log-prob in its last slots), and a NaN or
  *            +inf anywhere in a row makes its log-probs NaN, as log_softmax
  *            does.
+ *   splits   workgroups per row (0 = chosen from rows and vocab so that the
+ *            grid covers the GPU); with more than one, each writes its
+ *            slice's top k and log-sum-exp into workspace and a second
+ *            kernel merges them
+ *   workspace / workspace_bytes  at least
+ *            cast_draft_topk_workspace_size(rows, vocab, dtype, k, splits)
+ *            bytes, 16-byte aligned (may be NULL when that size is 0)
  * cast_build_trees replaces build_tree (cast_trees/tree.py:29-49), one tree
  * per request, the same heap order (-score, depth, parent, rank, counter):
  *   top_idx / top_lp  [batch][L][k] as written by cast_draft_topk; top_lp
@@ -255,8 +262,10 @@ int cast_store_append(const void *const *k_pack, const void *const *v_pack, void
  *   others a scan of every pushed candidate; both pop the heap's order.
  * ------------------------------------------------------------------- */
 int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t rows, int32_t vocab,
-                    int32_t dtype, int32_t k, int64_t *top_idx, float *top_lp,
-                    cast_stream_t stream);
+                    int32_t dtype, int32_t k, int64_t *top_idx, float *top_lp, int32_t splits,
+                    void *workspace, size_t workspace_bytes, cast_stream_t stream);
+size_t cast_draft_topk_workspace_size(int32_t rows, int32_t vocab, int32_t dtype, int32_t k,
+                                      int32_t splits);
 int cast_build_trees(const int64_t *top_idx, const void *top_lp, int32_t lp_dtype, int32_t batch,
                      int32_t L, int32_t k, const int32_t *budget, int64_t *token, int32_t *depth,
                      int32_t *parent, double *score, int32_t *n_nodes, int32_t *status,

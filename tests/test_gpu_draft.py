@@ -27,14 +27,15 @@ def test_topk_marginals_match_oracle(gpu, dtype, k):
     x = rng.normal(scale=5.0, size=(15, 151936)).astype(np.float32)
     x[3, [10, 99, 151935]] = x[3].max() + 2.0          # ties at the top of one row
     xd = torch.from_numpy(x).to(gpu).to(dtype)
-    print(f"case topk {dtype} k={k}", flush=True)
-    idx, lp = topk_marginals(xd, k, on_device=True)
-    torch.cuda.synchronize()
     want_i, want_lp = OD.topk_log_softmax(xd.float().cpu().numpy(), k)
-    assert idx.cpu().numpy().tolist() == want_i.tolist()
-    assert np.abs(lp.cpu().numpy() - want_lp).max() <= 2e-5
-    if dtype == torch.float32:
-        assert idx[3, :3].cpu().tolist() == [10, 99, 151935]
+    for splits in (0, 1, 3, 4):   # one workgroup per row, and rows split across workgroups
+        print(f"case topk {dtype} k={k} splits={splits}", flush=True)
+        idx, lp = topk_marginals(xd, k, on_device=True, splits=splits)
+        torch.cuda.synchronize()
+        assert idx.cpu().numpy().tolist() == want_i.tolist(), f"splits={splits}"
+        assert np.abs(lp.cpu().numpy() - want_lp).max() <= 2e-5, f"splits={splits}"
+        if dtype == torch.float32:
+            assert idx[3, :3].cpu().tolist() == [10, 99, 151935]
     # the drop-in returns host tensors like the reference
     hi, hl = topk_marginals(xd, k)
     assert hi.device.type == "cpu" and torch.equal(hi, idx.cpu())
@@ -43,11 +44,11 @@ def test_topk_marginals_match_oracle(gpu, dtype, k):
 @pytest.mark.parametrize("dtype,V,pad", [(torch.float32, 151936, 0), (torch.bfloat16, 151936, 0),
                                          (torch.bfloat16, 1000, 3), (torch.float32, 50000, 1)])
 def test_topk_marginals_edge_rows(gpu, dtype, V, pad):
-    # all-equal, increasing, decreasing, mostly -inf and integer-tied rows;
+    # all-equal, increasing, decreasing, mostly -inf, integer-tied, NaN and +inf rows;
     # small vocabularies and unaligned row strides take the scalar path
     from cast_amd.draft import topk_marginals
     rng = np.random.default_rng(V + pad)
-    x = np.empty((6, V + pad), dtype=np.float32)
+    x = np.empty((8, V + pad), dtype=np.float32)
     x[0] = 0.0
     x[1] = np.arange(V + pad) / 7.0
     x[2] = -np.arange(V + pad) / 7.0
@@ -55,16 +56,22 @@ def test_topk_marginals_edge_rows(gpu, dtype, V, pad):
     x[3, rng.integers(0, V, size=5)] = rng.normal(size=5)
     x[4] = np.round(rng.normal(scale=3.0, size=V + pad))
     x[5] = rng.normal(size=V + pad)
+    x[6] = rng.normal(size=V + pad)     # a NaN never ranks and makes the row's log-probs NaN
+    x[6, V // 3] = np.nan
+    x[7] = rng.normal(size=V + pad)     # +inf ranks first; log-probs NaN as in log_softmax
+    x[7, V // 2] = np.inf
     xd = torch.from_numpy(x).to(gpu).to(dtype)[:, :V]
     print(f"case topk-edge {dtype} V={V} ld={xd.stride(0)}", flush=True)
     for k in (1, 8, 16):
-        idx, lp = topk_marginals(xd, k, on_device=True)
         want_i, want_lp = OD.topk_log_softmax(xd.float().cpu().numpy(), k)
-        assert idx.cpu().numpy().tolist() == want_i.tolist(), f"k={k}"
-        got = lp.cpu().numpy()
-        assert np.array_equal(np.isinf(got), np.isinf(want_lp))
-        fin = np.isfinite(want_lp)
-        assert np.abs(got[fin] - want_lp[fin]).max() <= 2e-5, f"k={k}"
+        for splits in (0, 1, 4):
+            idx, lp = topk_marginals(xd, k, on_device=True, splits=splits)
+            assert idx.cpu().numpy().tolist() == want_i.tolist(), f"k={k} splits={splits}"
+            got = lp.cpu().numpy()
+            assert np.array_equal(np.isinf(got), np.isinf(want_lp))
+            assert np.array_equal(np.isnan(got), np.isnan(want_lp))
+            fin = np.isfinite(want_lp)
+            assert np.abs(got[fin] - want_lp[fin]).max() <= 2e-5, f"k={k} splits={splits}"
 
 
 def test_build_trees_match_reference_fixtures(gpu):
