@@ -174,8 +174,7 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
 #pragma unroll
     for (int j = 0; j < K; ++j) tk[j] = 0;
     uint64_t thr = 1;           // every key but NaN's passes
-    float thr_v = -INFINITY;    // the threshold's value and index: an element passes
-    int thr_i = INT_MAX;        // if v > thr_v, or v == thr_v and its index <= thr_i
+    float thr_v = -INFINITY;    // the threshold's value
     auto insert = [&](uint64_t key) __attribute__((always_inline)) {   // keys are unique
         if (key > tk[K - 1]) {
             bool placed = false;
@@ -229,20 +228,22 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
         if constexpr (EPC == 8) m = fmaxf(m, fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
         return m;
     };
-    // the chunk's elements that pass, in index order, one insertion sequence for all
+    // the chunk's elements at or above the threshold's value, in index order;
+    // the exact key test (ties at the threshold value pass up to its index)
+    // is made at insertion
     auto filter = [&](const float (&v)[EPC], float m, int c) __attribute__((always_inline)) {
         if (m >= thr_v) {   // no element of the chunk passes otherwise
             uint32_t pm = 0;
 #pragma unroll
-            for (int e = 0; e < EPC; ++e)
-                pm |= ((v[e] > thr_v) | ((v[e] == thr_v) & (c * EPC + e <= thr_i)) ? 1u : 0u) << e;
+            for (int e = 0; e < EPC; ++e) pm |= (v[e] >= thr_v ? 1u : 0u) << e;
             while (pm) {
                 const int e = __builtin_ctz(pm);
                 pm &= pm - 1;
                 float ve = v[0];
 #pragma unroll
                 for (int e2 = 1; e2 < EPC; ++e2) ve = e == e2 ? v[e2] : ve;
-                insert(rank_key(ve, c * EPC + e));
+                const uint64_t key = rank_key(ve, c * EPC + e);
+                if (key >= thr) insert(key);
             }
         }
     };
@@ -292,7 +293,6 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
         if (t != 0) {   // NW * R >= k distinct real elements are at or above t
             thr = t;
             thr_v = key_value(t);
-            thr_i = key_index(t);
         }
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
