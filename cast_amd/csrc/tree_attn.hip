@@ -41,6 +41,7 @@ constexpr int kCombineFast = 4;          // splits the combine loads in one roun
 // head) units split down to two 64-key tiles per workgroup: a single request
 // at S=2048, P=16 takes 24.7 us per call at 128 keys against 32.3 us at 512.
 constexpr int kMinChunk = 128;
+constexpr int kQkAhead = 4;   // K operand reads in flight ahead of the QK MFMAs
 
 // Where the keys and values of request b, KV head h live.  Two layouts:
 //  concat (store == 0): one ragged [total_kv, Hkv, D] tensor per K and V;
@@ -503,6 +504,15 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                 s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[ds], s[kb], 0, 0, 0);
             }
         }
+        // issue order: the K operand reads run kQkAhead MFMAs ahead of
+        // their use (the default schedule issues them one or two ahead)
+        __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 0);   // DS reads
+#pragma unroll
+        for (int i = 0; i < 2 * DSTEPS - kQkAhead; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // one DS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
 
         // ---- visibility (pack tiles and partial tiles only).  Element e of
         // lane (l32, g) in block kb is key t0 + 32*kb + 4*g + off(e),
