@@ -41,7 +41,7 @@ constexpr int kCombineFast = 4;          // splits the combine loads in one roun
 // head) units split down to two 64-key tiles per workgroup: a single request
 // at S=2048, P=16 takes 24.7 us per call at 128 keys against 32.3 us at 512.
 constexpr int kMinChunk = 128;
-constexpr int kQkAhead = 4;   // K operand reads in flight ahead of the QK MFMAs
+constexpr int kQkAhead = 4;   // K and V^T operand reads in flight ahead of their MFMAs
 
 // Where the keys and values of request b, KV head h live.  Two layouts:
 //  concat (store == 0): one ragged [total_kv, Hkv, D] tensor per K and V;
@@ -585,6 +585,15 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                         &Vt[buf][(db * 32 + l32) * VPAD + kb * 32 + hf * 16 + g * 8]);
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb][hf], o[db], 0, 0, 0);
                 }
+        // the same for the V^T operand reads of the PV product; the
+        // exponentials stay free to fill the gaps
+        __builtin_amdgcn_sched_group_barrier(0x100, kQkAhead, 1);
+#pragma unroll
+        for (int i = 0; i < 4 * DB - kQkAhead; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 1);
     }
 
     if (!active) return;
