@@ -322,8 +322,9 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     // K tile [key][d].  V tile transposed, [d][key'], with the keys of every
     // 16-key group stored in the order (0-3, 8-11, 4-7, 12-15): a lane's eight
     // P^T k-slots are then eight consecutive columns (one 16-byte read).
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KPAD];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VPAD];
+    constexpr int NBUF = 2;
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[NBUF][BN * KPAD];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[NBUF][D * VPAD];
     __shared__ EpiArgs epi;
 
     // ---- which unit is this workgroup?  Work items are renumbered so that
@@ -481,19 +482,9 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         epi.Hq = a.Hq;
     }
     __syncthreads();
-    // the next tile's loads are in flight during the current tile's MFMA work
-    if (ntiles > 0) fetch(0);
-    for (int t = 0; t < ntiles; ++t) {
-        const int buf = t & 1;
-        const int t0 = tile_t0(t);
-        const int valid = tile_valid(t);
-        publish(buf);
-        __syncthreads();
-        if (t + 1 < ntiles) fetch(t + 1);
-        if (!active) continue;
-
-        // ---- S^T = K Q^T: two 32-key blocks x 32 queries
-        floatx16 s[2];
+    // ---- the three stages of a tile
+    // S^T = K Q^T: two 32-key blocks x 32 queries
+    auto qk = [&](int buf, floatx16 (&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             s[kb] = floatx16{};
@@ -513,10 +504,14 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // one DS read
         }
         __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
-
-        // ---- visibility (pack tiles and partial tiles only).  Element e of
+    };
+    // visibility, the online softmax in base 2 and the P^T operand of tile t
+    auto softmax = [&](int t, floatx16 (&s)[2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+        // visibility (pack tiles and partial tiles only).  Element e of
         // lane (l32, g) in block kb is key t0 + 32*kb + 4*g + off(e),
         // off(e) = 8*(e/4) + e%4; in a pack tile that is pack key t0 - S + ...
+        const int t0 = tile_t0(t);
+        const int valid = tile_valid(t);
         const bool pack_tile = t >= n_pre;
         if (pack_tile || valid < BN) {
 #pragma unroll
@@ -532,11 +527,10 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                 }
             }
         }
-
-        // ---- online softmax in base 2.  The running max m is shared by the
-        // two lanes (l32, 0) and (l32, 1) of a query; it only moves when a
-        // tile exceeds it by more than 2^kRescaleSlack somewhere in the wave,
-        // so the cross-lane exchange and the O rescale are rare.
+        // The running max m is shared by the two lanes (l32, 0) and (l32, 1)
+        // of a query; it only moves when a tile exceeds it by more than
+        // 2^kRescaleSlack somewhere in the wave, so the cross-lane exchange
+        // and the O rescale are rare.
         float lmax = s[0][0];
 #pragma unroll
         for (int e = 1; e < 16; ++e) lmax = fmaxf(lmax, s[0][e]);
@@ -552,7 +546,6 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             m = mn;
             msafe = m == -INFINITY ? 0.f : m;
         }
-        bf16x8 pb[2][2];   // [kb][half]: P^T operand, 8 k-slots each
         float acc = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -571,10 +564,11 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             }
         }
         lsum += acc;
-
-        // ---- O^T += V^T P^T over four 16-key slices.  Slot j of lane group g
-        // in slice (kb, hf) is key 32*kb + 16*hf + 8*(j/4) + 4*g + j%4, stored
-        // at column 32*kb + 16*hf + 8*g + j.
+    };
+    // O^T += V^T P^T over four 16-key slices.  Slot j of lane group g in
+    // slice (kb, hf) is key 32*kb + 16*hf + 8*(j/4) + 4*g + j%4, stored at
+    // column 32*kb + 16*hf + 8*g + j.
+    auto pv = [&](int buf, const bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -594,6 +588,21 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
         }
         __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 1);
+    };
+
+    // the next tile's loads are in flight during the current tile's MFMA work
+    if (ntiles > 0) fetch(0);
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t % NBUF;
+        publish(buf);
+        __syncthreads();
+        if (t + 1 < ntiles) fetch(t + 1);
+        if (!active) continue;
+        floatx16 s[2];
+        bf16x8 pb[2][2];
+        qk(buf, s);
+        softmax(t, s, pb);
+        pv(buf, pb);
     }
 
     if (!active) return;
