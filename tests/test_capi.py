@@ -168,3 +168,27 @@ def test_attention_wrappers_refuse_tensors_on_other_devices():
                                         [5], [4], torch.zeros(4, dtype=torch.int64))
     with pytest.raises(ValueError, match="one GPU"):
         tree_attn._require_on(torch.device("cuda", 0), k=torch.zeros(1))
+
+
+def test_draft_topk_split_sizing_and_validation(lib):
+    # automatic splits: about one workgroup per CU, at least one first batch
+    # (8 x 512 chunks) per split and splits * k <= 64 for the combine wave
+    part = 144                              # bytes per (row, split) record
+    V, BF16, FP32 = 151936, 0, 1
+    assert lib.cast_draft_topk_workspace_size(120, V, BF16, 8, 0) == 120 * 2 * part
+    assert lib.cast_draft_topk_workspace_size(15, V, BF16, 8, 0) == 15 * 4 * part   # capped by the vocabulary
+    assert lib.cast_draft_topk_workspace_size(300, V, BF16, 8, 0) == 0             # one workgroup per row
+    assert lib.cast_draft_topk_workspace_size(8, V, FP32, 16, 0) == 8 * 4 * part    # 16 x 4 = 64 keys
+    assert lib.cast_draft_topk_workspace_size(8, V, BF16, 8, 1) == 0
+    assert lib.cast_draft_topk_workspace_size(8, 1000, BF16, 8, 4) == 0             # short rows never split
+    assert lib.cast_draft_topk_workspace_size(0, V, BF16, 8, 0) == 0
+    fake = 0x10000                          # never dereferenced: every case fails before a launch
+    call = lambda rows=120, k=8, splits=0, ws=fake, wsb=120 * 2 * part: lib.cast_draft_topk(
+        fake, V, rows, V, BF16, k, fake, fake, splits, ws, wsb, None)
+    assert call(k=0) == 7 and call(k=17) == 7 and call(splits=-1) == 7
+    assert lib.cast_draft_topk(fake, V - 1, 120, V, BF16, 8, fake, fake, 0, fake, 1 << 20, None) == 7   # ld < vocab
+    assert lib.cast_draft_topk(fake, V, 120, V, 5, 8, fake, fake, 0, fake, 1 << 20, None) == 4          # dtype
+    assert call(rows=0) == 0
+    assert call(ws=None) == 1                               # two splits need the workspace
+    assert call(wsb=120 * 2 * part - 1) == 8                # one byte short
+    assert call(ws=fake + 8) == 6                           # 16-byte alignment
