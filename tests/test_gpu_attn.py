@@ -138,3 +138,42 @@ def test_metadata_errors_are_flagged_not_faulted(gpu):
     with pytest.raises(AssertionError):
         varlen_tree_attention(q, k[:, :1].expand(-1, 3, -1), v[:, :1].expand(-1, 3, -1), meta["cu_q"],
                               meta["cu_kv"], meta["prefix_len"], meta["pack_len"], mask)
+
+
+def test_request_order_is_irrelevant(gpu):
+    # a full-size property: each request is computed on its own, and the
+    # split plan depends only on batch totals, so reordering the requests of
+    # a packed batch reorders the outputs and LSE bit for bit
+    from cast_amd import varlen_tree_attention
+    wl = SC.qwen3_ragged(seed=5)
+    print(f"case request-order: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv}", flush=True)
+    q, k, v = wl.qkv(device=gpu)
+    words = torch.from_numpy(_words(wl).view(np.int64).copy()).to(gpu)
+    cu_q, cu_kv = list(wl.cu_q), list(wl.cu_kv)
+    perm = [3, 0, 7, 5, 1, 6, 2, 4][:wl.B]
+    assert sorted(perm) == list(range(wl.B))
+
+    def run(order):
+        qs = [q[cu_q[b]:cu_q[b + 1]] for b in order]
+        ks = [k[cu_kv[b]:cu_kv[b + 1]] for b in order]
+        vs = [v[cu_kv[b]:cu_kv[b + 1]] for b in order]
+        ws = [words[cu_q[b]:cu_q[b + 1]] for b in order]
+        lq = [int(cu_q[b + 1] - cu_q[b]) for b in order]
+        lk = [int(cu_kv[b + 1] - cu_kv[b]) for b in order]
+        cq = torch.tensor(np.concatenate([[0], np.cumsum(lq)]), dtype=torch.int32, device=gpu)
+        ck = torch.tensor(np.concatenate([[0], np.cumsum(lk)]), dtype=torch.int32, device=gpu)
+        pre = torch.tensor([int(wl.prefix_len[b]) for b in order], dtype=torch.int32, device=gpu)
+        pk = torch.tensor([int(wl.pack_len[b]) for b in order], dtype=torch.int32, device=gpu)
+        out, lse = varlen_tree_attention(torch.cat(qs), torch.cat(ks), torch.cat(vs), cq, ck, pre, pk,
+                                         torch.cat(ws), return_lse=True, check=True)
+        torch.cuda.synchronize()
+        return out, lse, lq
+
+    out0, lse0, lq0 = run(list(range(wl.B)))
+    out1, lse1, lq1 = run(perm)
+    start0 = np.concatenate([[0], np.cumsum(lq0)])
+    start1 = np.concatenate([[0], np.cumsum(lq1)])
+    for j, b in enumerate(perm):
+        a0, a1 = slice(start0[b], start0[b] + lq0[b]), slice(start1[j], start1[j] + lq1[j])
+        assert torch.equal(out0[a0], out1[a1]), f"request {b}"
+        assert torch.equal(lse0[a0], lse1[a1]), f"request {b}"
