@@ -259,8 +259,9 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
         for (int u = 0; u < NB; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c0 + u * NT) * 16);
     };
 
-    constexpr int R = K > 8 ? 2 : 1;   // best keys taken per wave for the threshold
+    constexpr int R = K > 8 ? 4 : 2;   // best keys taken per wave for the threshold
     __shared__ uint64_t thr_keys[NW * R];
+    __shared__ uint64_t thr_pick;
     int c = cb + tid;
     u32x4 nxt[NB];
     if (ce - cb >= NB * NT) {   // first batch: the threshold, then the batch through it
@@ -286,11 +287,20 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
             if (lane == 0) thr_keys[wv * R + r] = wb;
             if (best == wb) best = 0;
         }
+        if (tid == 0) thr_pick = 0;
         __syncthreads();
-        uint64_t t = thr_keys[0];
+        // the k-th largest of the NW * R keys (distinct, or 0): k distinct
+        // real elements are at or above it
+        if (tid < NW * R) {
+            const uint64_t mine = thr_keys[tid];
+            int above = 0;
 #pragma unroll
-        for (int i = 1; i < NW * R; ++i) t = thr_keys[i] < t ? thr_keys[i] : t;
-        if (t != 0) {   // NW * R >= k distinct real elements are at or above t
+            for (int j = 0; j < NW * R; ++j) above += thr_keys[j] > mine ? 1 : 0;
+            if (above == k - 1) thr_pick = mine;
+        }
+        __syncthreads();
+        const uint64_t t = thr_pick;
+        if (t != 0) {   // k distinct real elements are at or above t
             thr = t;
             thr_v = key_value(t);
         }
