@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kMaxPack) void tree_bitmask_kernel(
 
 using namespace cast;
 
-extern "C" int cast_abi_version(void) { return 2; }
+extern "C" int cast_abi_version(void) { return 3; }
 
 extern "C" const char *cast_status_string(int status) {
     switch (status) {

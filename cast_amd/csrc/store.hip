@@ -10,6 +10,9 @@
 // The reference issues two advanced-indexing copies per layer; here one
 // workgroup per (request, layer, KV head) moves 16-byte chunks, driven by the
 // greedy-accept kernel's device-side path / path_len (no host round trip).
+// The per-layer base addresses come from host arrays and travel in the
+// kernel arguments, up to 64 layers per launch: a decode loop whose pack
+// tensors are new every round pays no table upload and no host sync.
 //
 // Every workgroup loads all of its rows before it stores any (registers,
 // then a barrier), so the copy is also correct in place: pack and store may
@@ -21,12 +24,17 @@
 
 namespace cast {
 
+// Layers per launch: their four base addresses travel in the kernel
+// arguments (4 x 64 x 8 B = 2 KiB), so the call needs no device table.
+constexpr int kAppendLayersPerLaunch = 64;
+
 struct AppendArgs {
-    const void *const *k_pack;   // [layers] pack K of each layer
-    const void *const *v_pack;
-    void *const *k_store;        // [layers] store K of each layer
-    void *const *v_store;
-    int32_t layers, batch, total_q, cap, Hkv, chunks;   // chunks = 16-byte pieces per (row, head)
+    const void *k_pack[kAppendLayersPerLaunch];   // pack K of each layer of this launch
+    const void *v_pack[kAppendLayersPerLaunch];
+    void *k_store[kAppendLayersPerLaunch];        // store K of each layer
+    void *v_store[kAppendLayersPerLaunch];
+    int32_t batch, total_q, cap, Hkv, chunks;     // chunks = 16-byte pieces per (row, head)
+    int32_t first_launch;                         // writes new_len and the per-request flag
     const int32_t *src_row;      // [batch] packed row of request b's root (cu_q of its pack)
     const int32_t *path;         // [batch][path_stride] accepted node indices (-1 padded)
     int32_t path_stride;
@@ -49,10 +57,10 @@ __global__ __launch_bounds__(kAppendThreads) void store_append_kernel(AppendArgs
     const int root = a.src_row[b];
     const int count = n + 1;     // root + accepted nodes
     if (n < 0 || n >= kMaxPack || s0 < 0 || s0 + count > a.cap || root < 0 || root >= a.total_q) {
-        if (threadIdx.x == 0 && layer == 0 && h == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        if (threadIdx.x == 0 && layer == 0 && h == 0 && a.first_launch) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         return;
     }
-    if (threadIdx.x == 0 && layer == 0 && h == 0 && a.new_len) a.new_len[b] = s0 + count;
+    if (threadIdx.x == 0 && layer == 0 && h == 0 && a.first_launch && a.new_len) a.new_len[b] = s0 + count;
     const char *kp = static_cast<const char *>(a.k_pack[layer]) + (int64_t)h * a.kp_head;
     const char *vp = static_cast<const char *>(a.v_pack[layer]) + (int64_t)h * a.vp_head;
     char *ks = static_cast<char *>(a.k_store[layer]) + (int64_t)b * a.ks_batch + (int64_t)h * a.ks_head;
@@ -119,12 +127,9 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     const int64_t strides[10] = {kp_tok, kp_head, vp_tok, vp_head, ks_batch, ks_head, ks_tok, vs_batch, vs_head, vs_tok};
     for (int64_t s : strides)
         if ((s * esz) % 16) return CAST_ERR_ALIGNMENT;
+    for (int32_t l = 0; l < layers; ++l)
+        if (!k_pack[l] || !v_pack[l] || !k_store[l] || !v_store[l]) return CAST_ERR_NULL_POINTER;
     AppendArgs a{};
-    a.k_pack = k_pack;
-    a.v_pack = v_pack;
-    a.k_store = k_store;
-    a.v_store = v_store;
-    a.layers = layers;
     a.batch = batch;
     a.total_q = total_q;
     a.cap = cap;
@@ -147,7 +152,18 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     a.vs_head = vs_head * esz;
     a.vs_tok = vs_tok * esz;
     a.status = status;
-    store_append_kernel<<<dim3(batch, layers, num_kv_heads), kAppendThreads, 0,
-                          reinterpret_cast<hipStream_t>(stream)>>>(a);
-    return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
+    for (int32_t l0 = 0; l0 < layers; l0 += kAppendLayersPerLaunch) {
+        const int32_t n = layers - l0 < kAppendLayersPerLaunch ? layers - l0 : kAppendLayersPerLaunch;
+        for (int32_t l = 0; l < n; ++l) {
+            a.k_pack[l] = k_pack[l0 + l];
+            a.v_pack[l] = v_pack[l0 + l];
+            a.k_store[l] = k_store[l0 + l];
+            a.v_store[l] = v_store[l0 + l];
+        }
+        a.first_launch = l0 == 0;
+        store_append_kernel<<<dim3(batch, n, num_kv_heads), kAppendThreads, 0,
+                              reinterpret_cast<hipStream_t>(stream)>>>(a);
+        if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
+    }
+    return CAST_OK;
 }

@@ -68,6 +68,7 @@ struct AttnArgs {
     const uint64_t *mask;
     int32_t mask_words;
     int32_t batch, total_q, total_kv, Hq, Hkv, G;
+    int32_t D, esz;     // head dim, bytes per element of q/out
     int64_t q_tok, q_head, o_tok, o_head;
     float scale_log2;   // sm_scale * log2(e)
     int32_t chunk;      // keys per split, multiple of 64 (kNoSplit = no split)
@@ -166,30 +167,83 @@ __device__ __forceinline__ Seq shfl_seq(const Seq &t, int src) {
 // Work items are ordered (b, h, split, row block) with the row block fastest.
 __device__ __forceinline__ int64_t items_of(const AttnArgs &a, const Seq &t) { return (int64_t)a.Hkv * t.ns * t.rb; }
 
-// Total work items and key rows of the valid requests.  Wave 0 of the
-// workgroup reports invalid requests.
-__device__ void batch_totals(const AttnArgs &a, int64_t &items, int64_t &kv_sum) {
+// Totals over the requests that pass load_seq (work items, key rows, query
+// rows), and whether any request failed it.  Wave 0 of the workgroup reports
+// invalid requests.
+struct BatchTotals {
+    int64_t items, kv_sum, q_sum;
+    bool bad;          // some request failed load_seq
+    bool unordered;    // cu_q decreases somewhere: accepted packs might overlap
+};
+
+__device__ BatchTotals batch_totals(const AttnArgs &a) {
     const int lane = threadIdx.x & 63;
-    items = 0;
-    kv_sum = 0;
+    BatchTotals r{0, 0, 0, false, false};
     for (int b0 = 0; b0 < a.batch; b0 += 64) {
         const int b = b0 + lane;
         Seq t;
         const bool ok = b < a.batch && load_seq(a, b, t, threadIdx.x < 64);
-        items += bcast64(wave_scan(ok ? items_of(a, t) : 0), 63);
-        kv_sum += bcast64(wave_scan(ok ? t.T : 0), 63);
+        r.items += bcast64(wave_scan(ok ? items_of(a, t) : 0), 63);
+        r.kv_sum += bcast64(wave_scan(ok ? t.T : 0), 63);
+        r.q_sum += bcast64(wave_scan(ok ? t.P : 0), 63);
+        r.bad |= __ballot(b < a.batch && !ok) != 0;
+        r.unordered |= __ballot(b < a.batch && a.cu_q[b + 1] < a.cu_q[b]) != 0;
     }
+    return r;
 }
 
-// In the store layout total_kv is a caller-supplied bound on sum(S_b + P_b)
-// that sized the grid and the workspace; a batch exceeding it is rejected
-// whole.  (The concat layout checks every request against it in load_seq.)
-__device__ __forceinline__ bool store_total_ok(const AttnArgs &a, int64_t kv_sum) {
-    if (a.kv.store && kv_sum > a.total_kv) {
+// total_q and total_kv are host-side bounds that sized the grid and the
+// workspace.  Accepted requests whose rows or keys add up past them overlap
+// (or the store layout's bound is too small), and a decreasing cu_q lets
+// packs overlap: such a batch is rejected whole.  Otherwise the accepted
+// packs are disjoint row ranges.
+__device__ __forceinline__ bool batch_fits(const AttnArgs &a, const BatchTotals &t) {
+    if (t.kv_sum > a.total_kv || t.q_sum > a.total_q || t.unordered) {
         if (threadIdx.x == 0) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         return false;
     }
     return true;
+}
+
+__device__ bool find_request(const AttnArgs &a, int64_t w, bool by_token, Seq &s, int &local);
+
+// Rows that no accepted request owns - those of rejected requests, rows
+// outside every request, or all rows of a rejected batch - get zeros and
+// lse = -inf, so an inconsistent call never returns uninitialised memory.
+// Every wave of the grid takes a share of the packed rows; the kernels call
+// this only when some request was rejected or the accepted ones leave rows
+// uncovered.
+__device__ void fill_unowned_rows(const AttnArgs &a, bool batch_ok) {
+    const int lane = threadIdx.x & 63;
+    const int waves = blockDim.x >> 6;
+    const int64_t first = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6);
+    const int64_t stride = (int64_t)gridDim.x * waves;
+    const int n = a.Hq * a.D;
+    for (int64_t t = first; t < a.total_q; t += stride) {
+        Seq s;
+        int local;
+        if (batch_ok && find_request(a, t, true, s, local)) continue;
+        char *row = static_cast<char *>(a.out) + t * a.o_tok * a.esz;
+        for (int e = lane; e < n; e += 64) {
+            char *p = row + ((int64_t)(e / a.D) * a.o_head + e % a.D) * a.esz;
+            if (a.esz == 2)
+                *reinterpret_cast<uint16_t *>(p) = 0;
+            else
+                *reinterpret_cast<float *>(p) = 0.f;
+        }
+        if (a.lse)
+            for (int h = lane; h < a.Hq; h += 64) a.lse[t * a.Hq + h] = -INFINITY;
+    }
+}
+
+// The start of every attention kernel: the batch totals, the fill of
+// unowned rows when needed; false when the batch is rejected whole.
+__device__ bool batch_prologue(const AttnArgs &a, int64_t &items) {
+    const BatchTotals t = batch_totals(a);
+    const bool ok = batch_fits(a, t);
+    if (!ok || t.bad || t.q_sum != a.total_q) fill_unowned_rows(a, ok);
+    items = t.items;
+    return ok;
 }
 
 // The request holding work item w (or, with by_token, packed row w), with its
@@ -333,9 +387,8 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     Seq sq;
     int local;
     {
-        int64_t total, kv_sum;
-        batch_totals(a, total, kv_sum);
-        if (!store_total_ok(a, kv_sum)) return;
+        int64_t total;
+        if (!batch_prologue(a, total)) return;
         const int64_t n8 = (total + 7) & ~(int64_t)7;
         const int64_t x = blockIdx.x;
         if (x >= n8) return;
@@ -659,10 +712,10 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     const int h0 = (blockIdx.x % groups) * hpg;
     Seq sq;
     int i;
-    if (a.kv.store) {
-        int64_t items, kv_sum;
-        batch_totals(a, items, kv_sum);
-        if (!store_total_ok(a, kv_sum)) return;
+    {
+        // a rejected batch was zero-filled by the attention kernel
+        const BatchTotals t = batch_totals(a);
+        if (t.kv_sum > a.total_kv || t.q_sum > a.total_q || t.unordered) return;
     }
     if (!find_request(a, tok, true, sq, i) || sq.ns <= 1) return;
     if (sq.part_off + (int64_t)sq.ns * sq.P > a.part_rows) return;
@@ -768,9 +821,8 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
     Seq sq;
     int local;
     {
-        int64_t total, kv_sum;
-        batch_totals(a, total, kv_sum);
-        if (!store_total_ok(a, kv_sum)) return;
+        int64_t total;
+        if (!batch_prologue(a, total)) return;
         if (!find_request(a, blockIdx.x, false, sq, local)) return;
     }
     const int rb = local % sq.rb;
@@ -976,6 +1028,8 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
     a.G = num_q_heads / num_kv_heads;
+    a.D = head_dim;
+    a.esz = (int32_t)esz;
     a.q_tok = q_tok;
     a.q_head = q_head;
     a.o_tok = o_tok;

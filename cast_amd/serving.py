@@ -33,6 +33,7 @@ bf16 inputs, tree_attn.py:66,87).
 """
 from __future__ import annotations
 
+import ctypes
 import weakref
 
 import numpy as np
@@ -44,34 +45,55 @@ from .tree_attn import store_tree_attention
 from .verify import tree_bitmask
 
 
-class VarlenPlan:
-    """State of one ragged verify pass, read by the attention hook below."""
-    active = False
+class VerifyPassState:
+    """Everything the attention hook reads while one batched verify forward
+    runs: the per-layer stores, the packed metadata and the index of the
+    next layer.  ``set`` arms the hook with those fields; ``clear`` disarms
+    it and drops the store references.  (The method names are the ones the
+    reference's server calls, cast_trees/serving.py:244, 253.)"""
 
-    def set(self, **kw):
-        self.__dict__.update(kw)
+    def __init__(self):
+        self.active = False
+        self.layer = 0
+        self.workspace = None
+
+    def set(self, **fields):
+        for name, value in fields.items():
+            setattr(self, name, value)
         self.layer = 0
         self.active = True
 
     def clear(self):
         self.active = False
-        self.buf_k = self.buf_v = None
+        self.buf_k = None
+        self.buf_v = None
         self.workspace = None
 
 
-PLAN = VarlenPlan()
-PACK_KV = {"k": [], "v": []}    # post-RoPE pack K/V of every layer, filled during the pass
+PLAN = VerifyPassState()
+# Per-layer K and V of the packed tree tokens (rotary already applied), as the
+# current verify forward hands them to the hook: PACK_KV["k"][layer] is
+# [Hkv, total_q, D].  The accepted-path append reads them after the forward.
+PACK_KV = {"k": [], "v": []}
+
+
+def _plain_attention(query, key, value, attention_mask, scaling):
+    """A forward that is not a tree verify (prefill, ordinary decode): torch
+    SDPA on HF's [1, H, n, D] layout, causal when there is no mask and more
+    than one query, handed back token-major as HF's attention callees do."""
+    mask = None if isinstance(attention_mask, bool) else attention_mask
+    causal = mask is None and query.shape[2] > 1
+    o = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling, is_causal=causal,
+                                       enable_gqa=True)
+    return o.transpose(1, 2).contiguous(), None
 
 
 def _varlen_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kw):
     """HF attention callee: query [1, Hq, total_q, D], key/value [1, Hkv, total_q, D]
-    -> ([1, total_q, Hq, D], None)."""
+    -> ([1, total_q, Hq, D], None).  Outside a verify pass (cast_trees/
+    serving.py:49-55) it is plain SDPA."""
     if not PLAN.active:
-        # prefill and any other forward: plain SDPA (cast_trees/serving.py:49-55)
-        mask = attention_mask if not isinstance(attention_mask, bool) else None
-        o = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling,
-                                           is_causal=mask is None and query.shape[2] > 1, enable_gqa=True)
-        return o.transpose(1, 2).contiguous(), None
+        return _plain_attention(query, key, value, attention_mask, scaling)
 
     li = PLAN.layer
     PLAN.layer += 1
@@ -156,75 +178,92 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
 
 # ---- accepted-path KV append (cast_trees/serving.py:264-289)
 
-_APPEND_LAYOUTS = {}   # (id, address) of every per-layer tensor -> (weakrefs, checked layout)
+_STORE_LAYOUTS = {}   # (id, address) of every per-layer store tensor -> (weakrefs, checked layout)
 
 
-def _append_layout(buf_k, buf_v, pack_k, pack_v):
-    """Check the per-layer stores and packs once and build the device table
-    of their base addresses.  The result is reused while the same tensor
-    objects sit at the same addresses (weak references tell a live object
-    from a new one that got a freed object's id), so a decode loop that keeps
-    its buffers pays the per-layer checks and the table copy once."""
+def _ptr_array(tensors):
+    """Host array of the tensors' device addresses (the C ABI copies it into
+    the kernel arguments)."""
+    return (ctypes.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
+
+
+def _store_layout(buf_k, buf_v):
+    """Check the per-layer stores once and keep their address arrays.  The
+    stores of a decode loop persist across rounds, so the result is reused
+    while the same tensor objects sit at the same addresses (weak references
+    tell a live object from a new one that got a freed object's id)."""
     L = len(buf_k)
-    if not (len(buf_v) == len(pack_k) == len(pack_v) == L) or L == 0:
-        raise ValueError("one store and one pack K/V tensor per layer")
-    tensors = (*pack_k, *pack_v, *buf_k, *buf_v)
+    if len(buf_v) != L or L == 0:
+        raise ValueError("one K and one V store per layer")
+    tensors = (*buf_k, *buf_v)
     key = tuple((id(t), t.data_ptr()) for t in tensors)
-    hit = _APPEND_LAYOUTS.get(key)
+    hit = _STORE_LAYOUTS.get(key)
     if hit is not None and all(r() is t for r, t in zip(hit[0], tensors)):
         return hit[1]
-    k0, p0 = buf_k[0], pack_k[0]
+    k0 = buf_k[0]
     B, Hkv, cap, D = (int(x) for x in k0.shape)
-    total_q = int(p0.shape[1])
-    for t in (*buf_k, *buf_v):
+    for t in tensors:
         if tuple(t.shape) != (B, Hkv, cap, D) or t.stride() != k0.stride() or t.dtype != k0.dtype:
             raise ValueError("every layer's store must share shape, strides and dtype")
-    for t in (*pack_k, *pack_v):
-        if tuple(t.shape) != (Hkv, total_q, D) or t.stride() != p0.stride() or t.dtype != k0.dtype:
-            raise ValueError(f"pack K/V must be [{Hkv}, total_q, {D}] with the store's dtype, alike in every layer")
-        if t.stride(-1) != 1 or t.data_ptr() % 16:
-            raise ValueError("pack K/V need a contiguous, 16-byte aligned head dim")
-    if k0.stride(-1) != 1 or any(t.data_ptr() % 16 for t in (*buf_k, *buf_v)):
-        raise ValueError("the store needs a contiguous, 16-byte aligned head dim")
-    for t in tensors:
         if t.device != k0.device:
-            raise ValueError("stores and packs must be on one device")
-    ptrs = torch.tensor([t.data_ptr() for t in tensors], dtype=torch.int64, device=k0.device)
-    layout = dict(ptrs=ptrs, L=L, B=B, Hkv=Hkv, cap=cap, D=D, total_q=total_q, dtype=k0.dtype, device=k0.device,
-                  pack_k=(p0.stride(1), p0.stride(0)), pack_v=(pack_v[0].stride(1), pack_v[0].stride(0)),
-                  store_k=tuple(k0.stride()[:3]), store_v=tuple(buf_v[0].stride()[:3]))
-    if len(_APPEND_LAYOUTS) >= 8:
-        _APPEND_LAYOUTS.clear()
-    _APPEND_LAYOUTS[key] = (tuple(weakref.ref(t) for t in tensors), layout)
+            raise ValueError("every layer's store must be on one device")
+    if k0.stride(-1) != 1 or any(t.data_ptr() % 16 for t in tensors):
+        raise ValueError("the store needs a contiguous, 16-byte aligned head dim")
+    layout = dict(k=_ptr_array(buf_k), v=_ptr_array(buf_v), L=L, B=B, Hkv=Hkv, cap=cap, D=D, dtype=k0.dtype,
+                  device=k0.device, store_k=tuple(k0.stride()[:3]), store_v=tuple(buf_v[0].stride()[:3]))
+    if len(_STORE_LAYOUTS) >= 8:
+        _STORE_LAYOUTS.clear()
+    _STORE_LAYOUTS[key] = (tuple(weakref.ref(t) for t in tensors), layout)
     return layout
 
 
+def _pack_arrays(lay, pack_k, pack_v):
+    """Check one round's pack K/V (new tensors every verify pass) against the
+    stores and return their address arrays, strides and total_q."""
+    L = lay["L"]
+    if len(pack_k) != L or len(pack_v) != L:
+        raise ValueError("one pack K and one pack V tensor per layer")
+    p0, v0 = pack_k[0], pack_v[0]
+    Hkv, D = lay["Hkv"], lay["D"]
+    total_q = int(p0.shape[1]) if p0.dim() == 3 else -1
+    want = (Hkv, total_q, D)
+    for ps, ref in ((pack_k, p0), (pack_v, v0)):
+        shape, stride = ref.shape, ref.stride()
+        if tuple(shape) != want or stride[-1] != 1:
+            raise ValueError(f"pack K/V must be [{Hkv}, total_q, {D}] with a contiguous head dim")
+        for t in ps:
+            if t.shape != shape or t.stride() != stride or t.dtype != lay["dtype"] or t.device != lay["device"]:
+                raise ValueError("pack K/V must share shape, strides, the store's dtype and device in every layer")
+    kp, vp = _ptr_array(pack_k), _ptr_array(pack_v)
+    if any(a % 16 for a in kp) or any(a % 16 for a in vp):
+        raise ValueError("pack K/V need 16-byte aligned rows")
+    return kp, vp, (p0.stride(1), p0.stride(0)), (v0.stride(1), v0.stride(0)), total_q
+
+
 def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_len, new_len, status=None):
-    """One cast_store_append launch over every layer (all arguments device
-    tensors; buf_* / pack_* lists of per-layer tensors)."""
+    """The KV append over every layer (all arguments device tensors; buf_* /
+    pack_* lists of per-layer tensors).  Stream-ordered, no host sync."""
     from . import _lib
     from .tree_attn import _DTYPES
     lib = _lib.load()
-    lay = _append_layout(buf_k, buf_v, pack_k, pack_v)
-    L, B = lay["L"], lay["B"]
+    lay = _store_layout(buf_k, buf_v)
     dev = lay["device"]
     if dev.type != "cuda":
         raise ValueError("the KV append runs on the GPU: stores and packs must be device tensors")
+    kp, vp, kp_st, vp_st, total_q = _pack_arrays(lay, pack_k, pack_v)
     for name, t in (("src_row", src_row), ("path", path), ("path_len", path_len), ("store_len", store_len),
                     ("new_len", new_len), ("status", status)):
         if t is not None and t.device != dev:
             raise ValueError(f"{name} must be on the stores' device {dev}")
     n = int(src_row.shape[0])
-    if n > B or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
+    if n > lay["B"] or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
         raise ValueError("path must be [B, >=128] (as written by greedy_accept) for B <= the store batch")
-    ptrs = lay["ptrs"]
-    pk, pv, sk, sv = (ptrs[i * L:(i + 1) * L] for i in range(4))
-    with torch.cuda.device(lay["device"]):
+    with torch.cuda.device(dev):
         st = lib.cast_store_append(
-            _lib.ptr(pk), _lib.ptr(pv), _lib.ptr(sk), _lib.ptr(sv), L, _lib.ptr(src_row), _lib.ptr(path),
-            path.stride(0), _lib.ptr(path_len), _lib.ptr(store_len), _lib.ptr(new_len), n, lay["total_q"],
-            lay["cap"], lay["Hkv"], lay["D"], *lay["pack_k"], *lay["pack_v"], *lay["store_k"], *lay["store_v"],
-            _DTYPES[lay["dtype"]], _lib.ptr(status), _lib.stream_of(buf_k[0]))
+            kp, vp, lay["k"], lay["v"], lay["L"], _lib.ptr(src_row), _lib.ptr(path), path.stride(0),
+            _lib.ptr(path_len), _lib.ptr(store_len), _lib.ptr(new_len), n, total_q, lay["cap"], lay["Hkv"],
+            lay["D"], *kp_st, *vp_st, *lay["store_k"], *lay["store_v"], _DTYPES[lay["dtype"]], _lib.ptr(status),
+            _lib.stream_of(buf_k[0]))
     _lib.check(st, "cast_store_append")
 
 
@@ -262,15 +301,24 @@ def append_store(buf_k, buf_v, store_len, cu_q, keep, accepted, rows):
     """
     dev = buf_k[0].device
     if len(rows) != len(store_len):
-        idx = torch.tensor(rows, dtype=torch.long, device=dev)
-        buf_k = [x[idx] for x in buf_k]
-        buf_v = [x[idx] for x in buf_v]
+        # requests that finished leave the batch: keep only the store rows of `rows`
+        survivors = torch.as_tensor(list(rows), dtype=torch.long, device=dev)
+        buf_k = [x.index_select(0, survivors) for x in buf_k]
+        buf_v = [x.index_select(0, survivors) for x in buf_v]
     new_len = [int(store_len[b]) + int(accepted[b]) for b in rows]
     cap = int(buf_k[0].shape[2])
-    if new_len and max(new_len) > cap:
-        new_cap = max(max(new_len), 2 * cap)
-        grow = lambda x: torch.cat([x, x.new_zeros(x.shape[0], x.shape[1], new_cap - cap, x.shape[3])], 2)
-        buf_k, buf_v = [grow(x) for x in buf_k], [grow(x) for x in buf_v]
+    need = max(new_len, default=0)
+    if need > cap:
+        # a slot would overflow: every store is widened to max(need, 2 * cap)
+        # slots, the new ones zero (the reference's growth rule)
+        wide = max(need, 2 * cap)
+
+        def widen(x):
+            y = x.new_zeros((x.shape[0], x.shape[1], wide, x.shape[3]))
+            y[:, :, :cap].copy_(x)
+            return y
+        buf_k = [widen(x) for x in buf_k]
+        buf_v = [widen(x) for x in buf_v]
     if not rows:
         return buf_k, buf_v, new_len
     path = np.full((len(rows), MAX_PACK), -1, dtype=np.int32)
@@ -335,10 +383,7 @@ def _tree_attention(module, query, key, value, attention_mask, scaling=None, dro
             and query.dtype in (torch.bfloat16, torch.float32)):
         meta = _tree_meta(attention_mask, int(key.shape[2]))
     if meta is None:
-        mask = attention_mask if not isinstance(attention_mask, bool) else None
-        o = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling,
-                                           is_causal=mask is None and query.shape[2] > 1, enable_gqa=True)
-        return o.transpose(1, 2).contiguous(), None
+        return _plain_attention(query, key, value, attention_mask, scaling)
     from .tree_attn import varlen_tree_attention
     cu_q, cu_kv, prefix_len, pack_len, words = meta
     out = varlen_tree_attention(query[0].transpose(0, 1), key[0].transpose(0, 1), value[0].transpose(0, 1),

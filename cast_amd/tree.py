@@ -28,10 +28,19 @@ MAX_PACK = 128          # two 64-bit ancestor words per packed token
 
 @dataclass
 class TreeNode:
+    """One drafted token of a candidate tree.
+
+    token   vocabulary id
+    depth   how many tokens after the pending root it sits (1 = a root child,
+            at most L, the drafter's block length)
+    parent  position of its parent in the same node list; -1 when the parent
+            is the root itself
+    score   summed drafter log-probabilities from the root down to this node
+    """
     token: int
-    depth: int      # distance from the pending root, 1..L
-    parent: int     # index into the node list, -1 = root
-    score: float    # path log-probability under the drafter marginals
+    depth: int
+    parent: int
+    score: float
 
 
 def _log_softmax64(x):
@@ -41,7 +50,8 @@ def _log_softmax64(x):
 
 
 def block_topk(logits, k=8):
-    """Top-k token ids and log-probs at each of the L future positions.
+    """Per future position (row of ``logits``, shape (L, V)): the k most
+    likely token ids and their log-softmax values, best first.
 
     Ties are broken towards the smaller token id (a stable descending sort).
     Only the k best columns are fully sorted: an ``argpartition`` picks every
@@ -65,7 +75,9 @@ def block_topk(logits, k=8):
 
 
 def build_tree(top_idx, top_lp, budget, k=8):
-    """Best-first prefix-closed tree with ``budget`` nonroot nodes.
+    """Grow a tree of ``budget`` nodes (root excluded) by always adding the
+    candidate with the highest path log-prob; a node joins only after its
+    parent, so every prefix of a path is in the tree.
 
     Candidates are expanded in order of path log-prob; equal scores fall back
     to (depth, parent, rank, insertion order), so the node order is fully

@@ -26,6 +26,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -55,6 +56,47 @@ def _mask_words(mask, total_q, device):
     if m.shape[0] != total_q:
         raise ValueError(f"ancestor_mask has {m.shape[0]} rows for {total_q} packed queries")
     return m.contiguous(), words
+
+
+def _host_side(x):
+    """Metadata the caller holds on the host (list, tuple, numpy, CPU tensor)."""
+    return not (isinstance(x, torch.Tensor) and x.is_cuda)
+
+
+def check_host_metadata(cu_q, prefix_len, pack_len, total_q, total_kv, words, cu_kv=None, cap=None):
+    """Validate host-side packing metadata before any launch (ValueError).
+
+    The rules are the ones the kernels apply to device-side metadata, where a
+    failure only skips the request (its rows come back as zeros with
+    lse = -inf): cu_q / cu_kv start at >= 0 and grow by each pack / by each
+    prefix + pack, stay within total_q / total_kv, and no pack is longer than
+    the ancestor words cover (64 tokens per word).  ``cap`` bounds the prefix
+    in the store layout.
+    """
+    cq = np.asarray(cu_q.cpu() if isinstance(cu_q, torch.Tensor) else cu_q, dtype=np.int64).reshape(-1)
+    S = np.asarray(prefix_len.cpu() if isinstance(prefix_len, torch.Tensor) else prefix_len,
+                   dtype=np.int64).reshape(-1)
+    P = np.asarray(pack_len.cpu() if isinstance(pack_len, torch.Tensor) else pack_len, dtype=np.int64).reshape(-1)
+    B = P.shape[0]
+    if cq.shape[0] != B + 1 or S.shape[0] != B:
+        raise ValueError("cu_q needs B+1 entries and prefix_len / pack_len B entries")
+    if B == 0:
+        return
+    if (P < 0).any() or (S < 0).any():
+        raise ValueError("negative prefix_len or pack_len")
+    if int(P.max()) > 64 * words:
+        raise ValueError(f"a pack of {int(P.max())} tokens exceeds the {64 * words} bits of the ancestor mask "
+                         f"({words} word{'s' if words > 1 else ''} per row)")
+    if cq[0] < 0 or not np.array_equal(np.diff(cq), P) or cq[-1] > total_q:
+        raise ValueError("cu_q must start at >= 0, grow by pack_len and end within total_q")
+    if cap is not None and int(S.max()) > cap:
+        raise ValueError(f"prefix_len exceeds the store capacity {cap}")
+    if cu_kv is not None:
+        ck = np.asarray(cu_kv.cpu() if isinstance(cu_kv, torch.Tensor) else cu_kv, dtype=np.int64).reshape(-1)
+        if ck.shape[0] != B + 1 or ck[0] < 0 or not np.array_equal(np.diff(ck), S + P) or ck[-1] > total_kv:
+            raise ValueError("cu_kv must start at >= 0, grow by prefix_len + pack_len and end within total_kv")
+    elif int((S + P).sum()) > total_kv:
+        raise ValueError("sum(prefix_len + pack_len) exceeds total_kv")
 
 
 def _require_on(dev, **tensors):
@@ -115,6 +157,9 @@ def varlen_tree_attention(q, k, v, cu_q, cu_kv, prefix_len, pack_len, ancestor_m
     dev = q.device
     _require_on(dev, k=k, v=v, out=out, workspace=workspace)
     q, k, v = _ready(q, esz), _ready(k, esz), _ready(v, esz)
+    mask, words = _mask_words(ancestor_mask, total_q, dev)
+    if any(_host_side(x) for x in (cu_q, cu_kv, prefix_len, pack_len)):
+        check_host_metadata(cu_q, prefix_len, pack_len, total_q, total_kv, words, cu_kv=cu_kv)
     cu_q = _as_i32(cu_q, dev)
     cu_kv = _as_i32(cu_kv, dev)
     prefix_len = _as_i32(prefix_len, dev)
@@ -122,7 +167,6 @@ def varlen_tree_attention(q, k, v, cu_q, cu_kv, prefix_len, pack_len, ancestor_m
     B = int(pack_len.shape[0])
     if cu_q.shape[0] != B + 1 or cu_kv.shape[0] != B + 1 or prefix_len.shape[0] != B:
         raise ValueError("cu_q / cu_kv need B+1 entries and prefix_len / pack_len B entries")
-    mask, words = _mask_words(ancestor_mask, total_q, dev)
     if out is None:
         out = torch.empty((total_q, H_q, D), dtype=q.dtype, device=dev)
     elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
@@ -197,15 +241,17 @@ def store_tree_attention(q, k_store, v_store, k_pack, v_pack, cu_q, prefix_len, 
     q, k_pack, v_pack = _ready(q, esz), _ready(k_pack, esz), _ready(v_pack, esz)
     if _ready(k_store, esz) is not k_store or _ready(v_store, esz) is not v_store:
         raise ValueError("the store needs a contiguous head dim and 16-byte aligned strides")
+    if total_kv is None:
+        total_kv = B * cap + total_q
+    total_kv = int(total_kv)
+    mask, words = _mask_words(ancestor_mask, total_q, dev)
+    if any(_host_side(x) for x in (cu_q, prefix_len, pack_len)):
+        check_host_metadata(cu_q, prefix_len, pack_len, total_q, total_kv, words, cap=cap)
     cu_q = _as_i32(cu_q, dev)
     prefix_len = _as_i32(prefix_len, dev)
     pack_len = _as_i32(pack_len, dev)
     if cu_q.shape[0] != B + 1 or prefix_len.shape[0] != B or pack_len.shape[0] != B:
         raise ValueError("cu_q needs B+1 entries and prefix_len / pack_len B entries (B = store batch)")
-    if total_kv is None:
-        total_kv = B * cap + total_q
-    total_kv = int(total_kv)
-    mask, words = _mask_words(ancestor_mask, total_q, dev)
     if out is None:
         out = torch.empty((total_q, H_q, D), dtype=q.dtype, device=dev)
     elif tuple(out.shape) != tuple(q.shape) or out.dtype != q.dtype or out.stride(-1) != 1:

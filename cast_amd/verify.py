@@ -18,6 +18,8 @@
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -142,24 +144,34 @@ def tree_attention_mask(n_prefix, nodes, device, dtype):
 
 
 def cache_layers(cache):
-    """(n_layers, get, put) over a DynamicCache: the per-layer objects of
-    recent transformers (``cache.layers[i].keys``) or the older
-    ``key_cache`` / ``value_cache`` lists."""
-    layers = getattr(cache, "layers", None)
-    if layers and hasattr(layers[0], "keys"):
+    """(n_layers, get, put) over a transformers DynamicCache.
+
+    Recent transformers keep one object per layer with ``.keys`` /
+    ``.values``; older releases keep two lists, ``key_cache`` and
+    ``value_cache``.  ``get(i)`` returns layer i's (K, V) and ``put(i, k, v)``
+    replaces them, whichever layout the cache has (cast_trees/verify.py:28-45
+    serves the same two layouts).
+    """
+    per_layer = getattr(cache, "layers", None)
+    if per_layer and hasattr(per_layer[0], "keys"):
         def get(i):
-            return layers[i].keys, layers[i].values
+            entry = per_layer[i]
+            return entry.keys, entry.values
 
         def put(i, k, v):
-            layers[i].keys, layers[i].values = k, v
-        return len(layers), get, put
+            entry = per_layer[i]
+            entry.keys = k
+            entry.values = v
+        return len(per_layer), get, put
+    k_list, v_list = cache.key_cache, cache.value_cache
 
     def get(i):
-        return cache.key_cache[i], cache.value_cache[i]
+        return k_list[i], v_list[i]
 
     def put(i, k, v):
-        cache.key_cache[i], cache.value_cache[i] = k, v
-    return len(cache.key_cache), get, put
+        k_list[i] = k
+        v_list[i] = v
+    return len(k_list), get, put
 
 
 def gather_cache(cache, n_prefix, keep):
@@ -205,23 +217,17 @@ def gather_cache(cache, n_prefix, keep):
         if any(a % 16 for a in addrs):
             raise ValueError("gather_cache: 16-byte aligned layers")
         L = n_layers
-        # one host-to-device copy: [pack K | pack V | store K | store V] addresses, then
-        # int32 src_row, path_len, store_len, new_len and the [1, MAX_PACK] path
-        host = np.zeros(4 * L + (4 + MAX_PACK + 1) // 2, dtype=np.int64)
-        host[:L] = [a + step for a in addrs[:L]]
-        host[L:2 * L] = [a + step for a in addrs[L:]]
-        host[2 * L:4 * L] = addrs
-        i32 = host[4 * L:].view(np.int32)
-        i32[:4] = (0, n - 1, n_prefix, 0)
-        i32[4:4 + MAX_PACK] = -1
-        i32[4:4 + n - 1] = [x - 1 for x in keep[1:]]
-        dev_buf = torch.from_numpy(host).to(k0.device)
-        d32 = dev_buf[4 * L:].view(torch.int32)
-        ptrs = dev_buf[:4 * L]
+        ptrs = lambda xs: (ctypes.c_void_p * L)(*xs)
+        # one host-to-device copy of the int32 metadata: src_row, path_len,
+        # store_len, new_len, then the [1, MAX_PACK] path
+        meta = np.full(4 + MAX_PACK, -1, dtype=np.int32)
+        meta[:4] = (0, n - 1, n_prefix, 0)
+        meta[4:4 + n - 1] = [x - 1 for x in keep[1:]]
+        d32 = torch.from_numpy(meta).to(k0.device)
         with torch.cuda.device(k0.device):
             st = lib.cast_store_append(
-                _lib.ptr(ptrs[:L]), _lib.ptr(ptrs[L:2 * L]), _lib.ptr(ptrs[2 * L:3 * L]),
-                _lib.ptr(ptrs[3 * L:]), L, _lib.ptr(d32[0:1]), _lib.ptr(d32[4:]), MAX_PACK,
+                ptrs([a + step for a in addrs[:L]]), ptrs([a + step for a in addrs[L:]]), ptrs(addrs[:L]),
+                ptrs(addrs[L:]), L, _lib.ptr(d32[0:1]), _lib.ptr(d32[4:]), MAX_PACK,
                 _lib.ptr(d32[1:2]), _lib.ptr(d32[2:3]), _lib.ptr(d32[3:4]), 1, n_pack, T, Hkv, D,
                 stride[2], stride[1], stride[2], stride[1], stride[0], stride[1], stride[2],
                 stride[0], stride[1], stride[2], _DTYPES[k0.dtype], None, _lib.stream_of(k0))

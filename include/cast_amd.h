@@ -95,7 +95,12 @@ int cast_tree_bitmask(const int32_t *parent, const int32_t *cu_q, int32_t batch,
  *   workspace / workspace_bytes  scratch of at least
  *             cast_tree_attn_workspace_size(...) bytes, 256-byte aligned
  *   status    int32*, nullable device status word
- * Rows with no visible key produce zeros and lse = -inf.
+ * Rows with no visible key produce zeros and lse = -inf.  So do the rows of
+ * every request the kernels reject on its device-side metadata (pack longer
+ * than 64 * mask_words, offsets that disagree with prefix_len / pack_len,
+ * keys beyond the row addressing) and rows outside every request; a batch
+ * whose accepted packs or keys exceed total_q / total_kv, or whose cu_q
+ * decreases, is rejected whole.  Rejections also raise *status bits.
  * ------------------------------------------------------------------- */
 int cast_tree_attn_fwd(const void *q, const void *k, const void *v, void *out, float *lse,
                        const int32_t *cu_q, const int32_t *cu_kv, const int32_t *prefix_len,
@@ -200,11 +205,14 @@ int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t vocab, int
  * K4: accepted-path KV append into the per-request store, every layer in
  * one launch.  Replaces the per-layer scatter of cast_trees/serving.py:
  * 264-289 (_append_store, two indexed copies per layer).
- *   k_pack / v_pack    device arrays of `layers` pointers to each layer's
- *                      pack K / V [Hkv, total_q, D] (strides kp_* / vp_*,
- *                      in elements, shared by all layers)
- *   k_store / v_store  device arrays of `layers` pointers to each layer's
- *                      store [batch, Hkv, cap, D] (strides ks_* / vs_*)
+ *   k_pack / v_pack    HOST arrays of `layers` device pointers to each
+ *                      layer's pack K / V [Hkv, total_q, D] (strides kp_* /
+ *                      vp_*, in elements, shared by all layers)
+ *   k_store / v_store  HOST arrays of `layers` device pointers to each
+ *                      layer's store [batch, Hkv, cap, D] (strides ks_* / vs_*)
+ *                      The addresses travel in the kernel arguments (64
+ *                      layers per launch), so the arrays may be reused or
+ *                      freed as soon as the call returns.
  *   src_row   int32 [batch]  packed row of request b's root (cu_q of its pack)
  *   path      int32 [batch][path_stride >= 128]  accepted node indices, as
  *             written by cast_greedy_accept;  path_len int32 [batch]

@@ -16,6 +16,9 @@ Contents, each restating the reference algorithm it cites:
                (cast_trees/decode.py:13-17, 85-103)
   draft.py     drafter top-k over the log-softmax and the best-first tree
                build (cast_trees/tree.py:20-49, cast_trees/verify.py:8-12)
+  store.py     accepted-path KV append and batch-one cache compaction, row
+               by row (cast_trees/serving.py:264-289, cast_trees/verify.py:
+               48-60)
 
 Pinning (what fixes each function independently of its own formula):
   bitmask  - reference int64 recurrence of serving.py:218-222 (a different
@@ -28,6 +31,9 @@ Pinning (what fixes each function independently of its own formula):
              (tests/golden/tree_fixtures.json: top-k ids and log-probs,
              trees of 15..127 nodes), exact; prefix-closure and descending
              scores along every root path.
+  store    - plain indexing checked bit for bit; tests/test_oracle.py pins
+             it on hand-built stores (untouched slots, growth zero-filled,
+             compaction order) and against index_select for gather_cache.
   walk     - replay-style accepted length (cast_trees/replay.py:20-32, a
              rank-tuple path-set formulation), planted-path workloads, and
              brute force over every root path on tiny trees.

@@ -27,7 +27,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert names == sorted(_lib.SIGNATURES), "ctypes bindings and header disagree"
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.cast_abi_version() == 2
+    assert lib.cast_abi_version() == 3
 
 
 def test_status_strings(lib):
@@ -118,25 +118,32 @@ def test_store_append_host_validation(lib):
     assert f(*args(B=0)) == 0 and f(*args(layers=0)) == 0
 
 
-def test_append_layout_checked_once_and_rechecked_on_change():
-    # the per-layer checks of the KV append run once per set of buffers; a
-    # replaced layer tensor (new object, other shape) is checked again
+def test_store_layout_checked_once_and_rechecked_on_change():
+    # the per-layer checks of the stores run once per set of stores; a
+    # replaced layer tensor (new object, other shape) is checked again.  The
+    # pack K/V are new tensors every verify pass and are checked per call.
     import torch
     from cast_amd import serving
     L = 4
     buf_k = [torch.empty((2, 2, 16, 64), dtype=torch.bfloat16) for _ in range(L)]
     buf_v = [torch.empty_like(x) for x in buf_k]
-    pack_k = [torch.empty((2, 5, 64), dtype=torch.bfloat16) for _ in range(L)]
-    pack_v = [torch.empty_like(x) for x in pack_k]
-    first = serving._append_layout(buf_k, buf_v, pack_k, pack_v)
-    assert serving._append_layout(buf_k, buf_v, pack_k, pack_v) is first
-    assert first["ptrs"].tolist() == [t.data_ptr() for t in (*pack_k, *pack_v, *buf_k, *buf_v)]
+    first = serving._store_layout(buf_k, buf_v)
+    assert serving._store_layout(buf_k, buf_v) is first
+    assert list(first["k"]) == [t.data_ptr() for t in buf_k]
+    assert list(first["v"]) == [t.data_ptr() for t in buf_v]
     buf_k[2] = torch.empty((2, 2, 8, 64), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="share shape"):
-        serving._append_layout(buf_k, buf_v, pack_k, pack_v)
+        serving._store_layout(buf_k, buf_v)
     buf_k[2] = torch.empty((2, 2, 16, 64), dtype=torch.bfloat16)
-    again = serving._append_layout(buf_k, buf_v, pack_k, pack_v)
-    assert again is not first and again["ptrs"][L * 2 + 2].item() == buf_k[2].data_ptr()
+    again = serving._store_layout(buf_k, buf_v)
+    assert again is not first and again["k"][2] == buf_k[2].data_ptr()
+    pack_k = [torch.empty((5, 2, 64), dtype=torch.bfloat16).transpose(0, 1) for _ in range(L)]
+    pack_v = [torch.empty_like(x) for x in pack_k]
+    kp, vp, kst, vst, total_q = serving._pack_arrays(again, pack_k, pack_v)
+    assert list(kp) == [t.data_ptr() for t in pack_k] and total_q == 5 and kst == (128, 64)
+    pack_v[1] = torch.empty((2, 5, 64), dtype=torch.float32)
+    with pytest.raises(ValueError, match="dtype"):
+        serving._pack_arrays(again, pack_k, pack_v)
 
 
 def test_build_trees_checks_inputs_before_launch():
@@ -192,3 +199,27 @@ def test_draft_topk_split_sizing_and_validation(lib):
     assert call(ws=None) == 1                               # two splits need the workspace
     assert call(wsb=120 * 2 * part - 1) == 8                # one byte short
     assert call(ws=fake + 8) == 6                           # 16-byte alignment
+
+
+def test_host_metadata_is_checked_before_launch():
+    # metadata already on the host (lists / numpy) is validated in Python:
+    # the call raises before any device work
+    import numpy as np
+    from cast_amd.tree_attn import check_host_metadata
+    ok = dict(cu_q=[0, 10, 30], prefix_len=[5, 7], pack_len=[10, 20], total_q=30, total_kv=42, words=2,
+              cu_kv=[0, 15, 42])
+    check_host_metadata(**ok)
+    with pytest.raises(ValueError, match="exceeds the 64 bits"):
+        check_host_metadata(**dict(ok, pack_len=[10, 70], cu_q=[0, 10, 80], total_q=80, cu_kv=[0, 15, 92],
+                                   total_kv=92, words=1))
+    with pytest.raises(ValueError, match="cu_q"):
+        check_host_metadata(**dict(ok, cu_q=[0, 11, 31]))
+    with pytest.raises(ValueError, match="cu_kv"):
+        check_host_metadata(**dict(ok, cu_kv=[0, 16, 43]))
+    with pytest.raises(ValueError, match="cu_q"):
+        check_host_metadata(**dict(ok, total_q=29))
+    with pytest.raises(ValueError, match="store capacity"):
+        check_host_metadata(**dict(ok, cu_kv=None, cap=6))
+    with pytest.raises(ValueError, match="total_kv"):
+        check_host_metadata(**dict(ok, cu_kv=None, total_kv=41))
+    check_host_metadata(**dict(ok, cu_q=np.array([0, 10, 30]), cu_kv=None))

@@ -1,43 +1,18 @@
 """Accepted-path KV append (cast_trees/serving.py:264-289) on the GPU.
 
-Bar: bit-identical stores and lengths against a torch restatement of the
-reference's _append_store (batch compaction, capacity growth, then per layer
-buf[dst_b, :, dst_p] = pack[:, src].permute(1, 0, 2)).
+Bar: bit-identical stores and lengths against the oracle's row-by-row
+restatement of the reference's _append_store (batch compaction, capacity
+growth, then every kept pack row into its store slot) and of gather_cache
+(cast_trees/verify.py:48-60).
 """
 import numpy as np
 import pytest
 import torch
 
 from cast_amd import scenarios as SC
+from oracle import store as OS
 
 pytestmark = pytest.mark.gpu
-
-
-def _reference_append(buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted, rows):
-    dev = buf_k[0].device
-    src, dst_b, dst_p, new_len = [], [], [], []
-    for nb, b in enumerate(rows):
-        for j, pk in enumerate(keep[b]):
-            src.append(cu_q[b] + pk)
-            dst_b.append(nb)
-            dst_p.append(store_len[b] + j)
-        new_len.append(store_len[b] + accepted[b])
-    if len(rows) != len(store_len):
-        idx = torch.tensor(rows, dtype=torch.long, device=dev)
-        buf_k = [x[idx] for x in buf_k]
-        buf_v = [x[idx] for x in buf_v]
-    cap = buf_k[0].shape[2]
-    if max(new_len) > cap:
-        new_cap = max(max(new_len), 2 * cap)
-        grow = lambda x: torch.cat([x, x.new_zeros(x.shape[0], x.shape[1], new_cap - cap, x.shape[3])], 2)
-        buf_k, buf_v = [grow(x) for x in buf_k], [grow(x) for x in buf_v]
-    src = torch.tensor(src, dtype=torch.long, device=dev)
-    dst_b = torch.tensor(dst_b, dtype=torch.long, device=dev)
-    dst_p = torch.tensor(dst_p, dtype=torch.long, device=dev)
-    for li in range(len(buf_k)):
-        buf_k[li][dst_b, :, dst_p] = pack_k[li][:, src].permute(1, 0, 2)
-        buf_v[li][dst_b, :, dst_p] = pack_v[li][:, src].permute(1, 0, 2)
-    return buf_k, buf_v, new_len
 
 
 def _setup(dev, seed, B=5, L=3, Hkv=4, D=128, cap=96, dtype=torch.bfloat16):
@@ -72,7 +47,7 @@ def test_append_store_matches_reference(gpu, case):
         store_len[1] = buf_k[0].shape[2] - 1          # one slot left: the append must grow the stores
         keep[1], accepted[1] = [0, 1, 2], 3
     print(f"case append-{case}: B={B} rows={rows} store_len={store_len} accepted={accepted}", flush=True)
-    ref = _reference_append([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
+    ref = OS.append_store([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
                             cu_q, keep, accepted, rows)
     serving.PACK_KV["k"], serving.PACK_KV["v"] = pack_k, pack_v
     got = serving.append_store([x.clone() for x in buf_k], [x.clone() for x in buf_v], store_len, cu_q, keep,
@@ -104,7 +79,7 @@ def test_append_accepted_from_greedy_accept(gpu):
     plen_h, path_h = plen.cpu().tolist(), path.cpu().tolist()
     keep = [[0] + [i + 1 for i in path_h[b][:plen_h[b]]] for b in range(wl.B)]
     accepted = [len(k) for k in keep]
-    ref = _reference_append([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
+    ref = OS.append_store([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
                             [int(x) for x in wl.cu_q], keep, accepted, list(range(wl.B)))
     assert new_len.cpu().tolist() == ref[2]
     assert max(accepted) > 1
@@ -122,15 +97,6 @@ def test_append_overflow_is_flagged(gpu):
     print("case append-overflow", flush=True)
     with pytest.raises(ValueError, match="inconsistent"):
         serving.append_accepted(buf_k, buf_v, [cap - 1, 0], cu_q, path, plen, pack_k, pack_v, check=True)
-
-
-def _reference_gather(layers, n_prefix, keep):
-    # cast_trees/verify.py:48-60: index_select of the prefix and the kept entries
-    dev = layers[0][0].device
-    sel = torch.arange(n_prefix, device=dev)
-    if keep:
-        sel = torch.cat([sel, torch.tensor([n_prefix + i for i in keep], device=dev)])
-    return [(k.index_select(2, sel), v.index_select(2, sel)) for k, v in layers]
 
 
 @pytest.mark.parametrize("case", ["path", "shift-by-one", "identity", "permuted", "root-only", "empty-prefix",
@@ -156,7 +122,7 @@ def test_gather_cache_matches_reference(gpu, case):
         keep = [0]
     else:
         keep = [0] + sorted(rng.choice(np.arange(1, n_pack), size=12, replace=False).tolist())
-    want = _reference_gather(layers, n_prefix, keep)
+    want = OS.gather_cache(layers, n_prefix, keep)
     if case == "old-layout":
         class _OldCache:
             pass

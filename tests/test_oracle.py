@@ -326,3 +326,47 @@ def test_draft_oracle_tree_invariants_and_ties():
         if p >= 0:
             assert nodes[p][1] == d - 1 and nodes[p][3] >= s         # a child never outscores its parent
     assert [n[3] for n in nodes] == sorted([n[3] for n in nodes], reverse=True)   # best-first pop order
+
+
+# ---- oracle/store.py: plain indexing, pinned on hand-built stores
+
+def test_store_append_oracle_known_answers():
+    import torch
+    from oracle import store as OS
+    B, Hkv, cap, D, total_q = 3, 2, 6, 4, 9
+    buf_k = [torch.arange(B * Hkv * cap * D, dtype=torch.float32).view(B, Hkv, cap, D)]
+    buf_v = [-buf_k[0]]
+    pack_k = [1000 + torch.arange(Hkv * total_q * D, dtype=torch.float32).view(Hkv, total_q, D)]
+    pack_v = [-pack_k[0]]
+    cu_q = [0, 3, 5, 9]
+    store_len = [2, 1, 3]
+    keep = [[0, 2], [0], [0, 1, 3]]
+    accepted = [2, 1, 3]
+    # requests 0 and 2 survive, no growth (3 + 3 = 6 = cap)
+    k, v, n = OS.append_store(buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted, [0, 2])
+    assert n == [4, 6] and k[0].shape == (2, Hkv, cap, D)
+    assert torch.equal(k[0][0, :, :2], buf_k[0][0, :, :2])          # old slots untouched
+    assert torch.equal(k[0][1, :, :3], buf_k[0][2, :, :3])          # request 2 moved to batch row 1
+    assert torch.equal(k[0][0, :, 2], pack_k[0][:, 0]) and torch.equal(k[0][0, :, 3], pack_k[0][:, 2])
+    assert torch.equal(k[0][1, :, 3], pack_k[0][:, 5]) and torch.equal(k[0][1, :, 5], pack_k[0][:, 8])
+    assert torch.equal(v[0], -k[0])
+    assert torch.equal(k[0][0, :, 4:], buf_k[0][0, :, 4:])          # slots past the new length untouched
+    # one more accepted row for request 2 overflows: stores double to 12 slots, zero-filled
+    k, v, n = OS.append_store(buf_k, buf_v, pack_k, pack_v, store_len, cu_q, [[0, 2], [0], [0, 1, 2, 3]],
+                              [2, 1, 4], [0, 1, 2])
+    assert n == [4, 2, 7] and k[0].shape == (3, Hkv, 12, D)
+    assert torch.equal(k[0][1, :, :1], buf_k[0][1, :, :1]) and torch.equal(k[0][1, :, 1], pack_k[0][:, 3])
+    assert torch.equal(k[0][1, :, 2:cap], buf_k[0][1, :, 2:cap])
+    assert torch.all(k[0][0, :, cap:] == 0) and torch.all(k[0][2, :, 7:] == 0)
+    assert torch.equal(k[0][2, :, 6], pack_k[0][:, 8])
+
+
+def test_gather_cache_oracle_matches_index_select():
+    import torch
+    from oracle import store as OS
+    g = torch.Generator().manual_seed(0)
+    layers = [(torch.randn(1, 2, 30, 8, generator=g), torch.randn(1, 2, 30, 8, generator=g)) for _ in range(3)]
+    keep = [0, 4, 5, 9, 17]
+    sel = torch.tensor(list(range(10)) + [10 + i for i in keep])
+    for (k, v), (kk, vv) in zip(layers, OS.gather_cache(layers, 10, keep)):
+        assert torch.equal(kk, k.index_select(2, sel)) and torch.equal(vv, v.index_select(2, sel))
