@@ -15,6 +15,8 @@ OK = 0
 ERR_HEAD_RATIO = 2
 ERR_PACK_TOO_LARGE = 3
 ERR_HIP = 10
+ERR_SCRATCH_LIMIT = 11
+ERR_DEVICE = 12
 
 FLAG_BAD_PACK = 1
 FLAG_BAD_OFFSETS = 2
@@ -40,6 +42,8 @@ SIGNATURES = {
     "cast_tree_attn_combine": (_ATTN_ARGS, ctypes.c_int),
     "cast_tree_attn_store_fwd": ([_P] * 11 + [_I32] * 8 + [_I64] * 14 + [_I32, ctypes.c_float, _I32, _P, _SZ, _P, _P],
                                  ctypes.c_int),
+    "cast_tree_attn_fwd_noalloc": (_ATTN_ARGS[:28] + _ATTN_ARGS[30:], ctypes.c_int),
+    "cast_tree_attn_noalloc_limit": ([], _SZ),
     "cast_tree_attn_workspace_size": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32], _SZ),
     "cast_tree_attn_default_split": ([_I32, _I32, _I32, _I32, _I32, _I32, _I32], _I32),
     "cast_store_append": ([_P] * 4 + [_I32] + [_P] * 2 + [_I32] + [_P] * 3 + [_I32] * 5 + [_I64] * 10 +

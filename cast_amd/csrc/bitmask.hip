@@ -74,6 +74,10 @@ extern "C" const char *cast_status_string(int status) {
         case CAST_ERR_WORKSPACE: return "workspace smaller than cast_tree_attn_workspace_size";
         case CAST_ERR_SCALE: return "softmax scale must be finite and positive";
         case CAST_ERR_HIP: return "a HIP runtime call or kernel launch failed";
+        case CAST_ERR_SCRATCH_LIMIT:
+            return "the split-K scratch this call needs exceeds the no-allocation entry point's static array "
+                   "(use a workspace, or a larger kv_split)";
+        case CAST_ERR_DEVICE: return "the stream belongs to another device than the current one";
         default: return "unknown status";
     }
 }

@@ -25,6 +25,7 @@
 #include <limits.h>
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "cast_common.hpp"
@@ -1166,4 +1167,72 @@ extern "C" int cast_tree_attn_store_fwd(const void *q, const void *k_store, cons
     return tree_attn_run(q, s, out, lse, cu_q, nullptr, prefix_len, pack_len, mask, mask_words, batch, total_q,
                          total_kv, num_q_heads, num_kv_heads, head_dim, q_tok, q_head, o_tok, o_head, dtype,
                          sm_scale, kv_split, workspace, workspace_bytes, status, stream, kStageAttn | kStageCombine);
+}
+
+// --------------------------------------------------------------------------
+// No-allocation entry point: the split-K partials live in a static device
+// array instead of a caller workspace, for callers that cannot allocate
+// (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc).  Each GPU the library runs on holds its own copy of the array
+// until the process ends.  Nothing in it must start at zero: every partial
+// row the combine reads is written by the attention kernel of the same call.
+// Calls that overlap on one GPU (other streams, other host threads) share
+// the array and race.
+// --------------------------------------------------------------------------
+namespace cast {
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace cast
+
+static __device__ __align__(256) unsigned char scratch[cast::kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[cast::kMaxDevices];   // device address of `scratch` per GPU
+
+// The array's device address on the current GPU, looked up once per device
+// with that device current.  The host-side name `scratch` is only a stand-in
+// and never reaches a kernel.
+int scratch_for_current_device(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= cast::kMaxDevices) return CAST_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return CAST_ERR_HIP;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CAST_OK;
+}
+}  // namespace
+
+extern "C" size_t cast_tree_attn_noalloc_limit(void) { return cast::kScratchBytes; }
+
+extern "C" int cast_tree_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *out, float *lse,
+                                          const int32_t *cu_q, const int32_t *cu_kv, const int32_t *prefix_len,
+                                          const int32_t *pack_len, const uint64_t *mask, int32_t mask_words,
+                                          int32_t batch, int32_t total_q, int32_t total_kv, int32_t num_q_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
+                                          int64_t k_tok, int64_t k_head, int64_t v_tok, int64_t v_head,
+                                          int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,
+                                          int32_t kv_split, int32_t *status, cast_stream_t stream) {
+    const size_t need = cast_tree_attn_workspace_size(batch, total_q, total_kv, num_q_heads, num_kv_heads,
+                                                      head_dim, dtype, kv_split);
+    if (need > cast::kScratchBytes) return CAST_ERR_SCRATCH_LIMIT;
+    void *ws = nullptr;
+    if (need) {
+        if (stream) {
+            int cur = -1, sdev = -1;
+            if (hipGetDevice(&cur) != hipSuccess ||
+                hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev) != hipSuccess)
+                return CAST_ERR_HIP;
+            if (cur != sdev) return CAST_ERR_DEVICE;
+        }
+        const int st = scratch_for_current_device(&ws);
+        if (st != CAST_OK) return st;
+    }
+    void *workspace = ws;
+    const size_t workspace_bytes = need ? cast::kScratchBytes : 0;
+    return CAST_CONCAT_RUN(kStageAttn | kStageCombine);
 }

@@ -39,7 +39,10 @@ enum cast_status {
     CAST_ERR_SHAPE = 7,            /* negative or inconsistent sizes */
     CAST_ERR_WORKSPACE = 8,        /* workspace smaller than the queried size */
     CAST_ERR_SCALE = 9,            /* softmax scale not finite and positive */
-    CAST_ERR_HIP = 10              /* a HIP runtime call or launch failed */
+    CAST_ERR_HIP = 10,             /* a HIP runtime call or launch failed */
+    CAST_ERR_SCRATCH_LIMIT = 11,   /* the no-allocation entry point would need more
+                                      split-K scratch than its static array holds */
+    CAST_ERR_DEVICE = 12           /* the stream's device is not the current device */
 };
 
 /* Bits a kernel ORs into the optional device status word (int32). */
@@ -168,6 +171,32 @@ int cast_tree_attn_store_fwd(const void *q, const void *k_store, const void *v_s
                              int64_t vp_tok, int64_t vp_head, int64_t o_tok, int64_t o_head,
                              int32_t dtype, float sm_scale, int32_t kv_split, void *workspace,
                              size_t workspace_bytes, int32_t *status, cast_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * cast_tree_attn_fwd without a workspace argument: allocates nothing.
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory during the call: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  The split-K partials go to a static
+ * device array of cast_tree_attn_noalloc_limit() bytes (64 MiB), which every
+ * GPU the library runs on holds until the process ends.  Calls whose
+ * cast_tree_attn_workspace_size(...) exceeds it return
+ * CAST_ERR_SCRATCH_LIMIT before any device work (a larger kv_split, or -1,
+ * needs less).  Call with the stream's device current (else
+ * CAST_ERR_DEVICE).  Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (other streams or host threads) race.  Arguments
+ * and results are otherwise those of cast_tree_attn_fwd, with the same
+ * kernels and the same output bits.
+ * ------------------------------------------------------------------- */
+int cast_tree_attn_fwd_noalloc(const void *q, const void *k, const void *v, void *out, float *lse,
+                               const int32_t *cu_q, const int32_t *cu_kv, const int32_t *prefix_len,
+                               const int32_t *pack_len, const uint64_t *mask, int32_t mask_words,
+                               int32_t batch, int32_t total_q, int32_t total_kv, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int64_t q_tok, int64_t q_head,
+                               int64_t k_tok, int64_t k_head, int64_t v_tok, int64_t v_head,
+                               int64_t o_tok, int64_t o_head, int32_t dtype, float sm_scale,
+                               int32_t kv_split, int32_t *status, cast_stream_t stream);
+/* Bytes of the static split-K scratch of cast_tree_attn_fwd_noalloc. */
+size_t cast_tree_attn_noalloc_limit(void);
 
 /* Workspace bytes cast_tree_attn_fwd needs for these host-known sizes. */
 size_t cast_tree_attn_workspace_size(int32_t batch, int32_t total_q, int32_t total_kv,

@@ -1,0 +1,63 @@
+"""The no-allocation entry point (split-K scratch in a static device array)
+against cast_tree_attn_fwd with a caller workspace: the same kernels, so
+outputs and LSE must agree bit for bit.  Two calls in a row, the second on a
+smaller input, so the second reuses (and must not depend on) what the first
+left in the shared array."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from cast_amd import _lib
+from cast_amd import scenarios as SC
+from oracle import bitmask as OB
+
+pytestmark = pytest.mark.gpu
+
+
+def _args(wl, dev, q, k, v, out, lse, mask, meta, kv_split):
+    return [_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(meta["cu_q"]),
+            _lib.ptr(meta["cu_kv"]), _lib.ptr(meta["prefix_len"]), _lib.ptr(meta["pack_len"]), _lib.ptr(mask), 2,
+            wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+            v.stride(0), v.stride(1), out.stride(0), out.stride(1), _lib.BF16, float(wl.D ** -0.5), kv_split]
+
+
+def _both(gpu, wl, kv_split=0):
+    lib = _lib.load()
+    q, k, v = wl.qkv(device=gpu)
+    meta = wl.meta_tensors(gpu)
+    mask = torch.from_numpy(OB.chain_walk_words(wl.packed.parent, wl.cu_q).view(np.int64).copy()).to(gpu)
+    need = lib.cast_tree_attn_workspace_size(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, _lib.BF16,
+                                             kv_split)
+    print(f"case noalloc {wl.name}: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv} scratch {need} B",
+          flush=True)
+    assert 0 < need <= lib.cast_tree_attn_noalloc_limit()
+    status = torch.zeros(2, dtype=torch.int32, device=gpu)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    out_a, out_b = torch.full_like(q, float("nan")), torch.full_like(q, float("nan"))
+    lse_a = torch.full(q.shape[:2], float("nan"), device=gpu)
+    lse_b = torch.full(q.shape[:2], float("nan"), device=gpu)
+    stream = _lib.stream_of(q)
+    with torch.cuda.device(gpu):
+        st = lib.cast_tree_attn_fwd(*_args(wl, gpu, q, k, v, out_a, lse_a, mask, meta, kv_split), _lib.ptr(ws),
+                                    need, _lib.ptr(status[0:1]), stream)
+        assert st == 0, _lib.status_string(st)
+        st = lib.cast_tree_attn_fwd_noalloc(*_args(wl, gpu, q, k, v, out_b, lse_b, mask, meta, kv_split),
+                                            _lib.ptr(status[1:2]), stream)
+        assert st == 0, _lib.status_string(st)
+    torch.cuda.synchronize()
+    assert status.tolist() == [0, 0]
+    assert torch.isfinite(out_a).all() and torch.isfinite(lse_a).all()
+    assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b)
+
+
+def test_noalloc_matches_workspace_entry_twice(gpu):
+    # a ragged batch that splits its prefixes, then a smaller single request
+    _both(gpu, SC.qwen3_ragged(seed=3, B=4, lo=100, hi=3000), kv_split=256)
+    _both(gpu, SC.qwen3_single(), kv_split=0)
+
+
+def test_noalloc_headline_shapes(gpu):
+    # the benchmark's shapes: 48 MiB of partials, within the 64 MiB array
+    _both(gpu, SC.qwen3_headline(), kv_split=0)
