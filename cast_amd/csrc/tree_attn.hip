@@ -86,7 +86,6 @@ struct AttnArgs {
 struct Seq {
     int b, S, P, T, q0, kv0, ns, rb, split_len;
     int64_t part_off;   // first partial row of this request (only if ns > 1)
-    int64_t unit_off;   // first (KV head, row block) unit of this request
 };
 
 // Reads and checks request b's metadata; `report` raises the device flags.
@@ -131,10 +130,6 @@ __device__ __forceinline__ bool load_seq(const AttnArgs &a, int b, Seq &s, bool 
 // holding request b0 + j, with wave prefix sums over the lanes, so that a
 // lookup costs one round of metadata loads per 64 requests.
 
-__device__ __forceinline__ int64_t shfl64(int64_t x, int src) {
-    const int lo = __shfl((int)(uint32_t)x, src), hi = __shfl((int)(x >> 32), src);
-    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
 // lane src's value in every lane, as a scalar (src wave-uniform)
 __device__ __forceinline__ int bcast(int x, int src) { return __builtin_amdgcn_readlane(x, src); }
 __device__ __forceinline__ int64_t bcast64(int64_t x, int src) {
@@ -142,15 +137,23 @@ __device__ __forceinline__ int64_t bcast64(int64_t x, int src) {
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(x >> 32), src);
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
-__device__ __forceinline__ int64_t wave_scan(int64_t x) {   // inclusive
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int64_t y = shfl64(x, lane >= off ? lane - off : lane);
-        if (lane >= off) x += y;
-    }
+// Inclusive scan over the 64 lanes of non-negative int32 values, saturating
+// at INT32_MAX (so inconsistent metadata can never wrap a sum to a small
+// value).  DPP row shifts build 16-lane scans, row broadcasts join them: all
+// VALU, no LDS round trips.
+__device__ __forceinline__ int wave_scan(int x) {
+    auto add = [](int a, int b) { return (int)min((uint32_t)a + (uint32_t)b, 0x7fffffffu); };
+    x = add(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false));   // row_shr:1
+    x = add(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false));   // row_shr:2
+    x = add(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false));   // row_shr:4
+    x = add(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false));   // row_shr:8
+    x = add(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));   // row_bcast:15 into rows 1, 3
+    x = add(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));   // row_bcast:31 into rows 2, 3
     return x;
 }
+// The saturated sum of x over the wave, in every lane.
+__device__ __forceinline__ int wave_sum(int x) { return bcast(wave_scan(x), 63); }
+
 __device__ __forceinline__ Seq shfl_seq(const Seq &t, int src) {
     Seq s;
     s.b = bcast(t.b, src);
@@ -166,7 +169,8 @@ __device__ __forceinline__ Seq shfl_seq(const Seq &t, int src) {
 }
 
 // Work items are ordered (b, h, split, row block) with the row block fastest.
-__device__ __forceinline__ int64_t items_of(const AttnArgs &a, const Seq &t) { return (int64_t)a.Hkv * t.ns * t.rb; }
+__device__ __forceinline__ int sat32(int64_t v) { return (int)min(v, (int64_t)0x7fffffff); }
+__device__ __forceinline__ int items_of(const AttnArgs &a, const Seq &t) { return sat32((int64_t)a.Hkv * t.ns * t.rb); }
 
 // Totals over the requests that pass load_seq (work items, key rows, query
 // rows), and whether any request failed it.  Wave 0 of the workgroup reports
@@ -182,11 +186,11 @@ __device__ BatchTotals batch_totals(const AttnArgs &a) {
     BatchTotals r{0, 0, 0, false, false};
     for (int b0 = 0; b0 < a.batch; b0 += 64) {
         const int b = b0 + lane;
-        Seq t;
+        Seq t{};
         const bool ok = b < a.batch && load_seq(a, b, t, threadIdx.x < 64);
-        r.items += bcast64(wave_scan(ok ? items_of(a, t) : 0), 63);
-        r.kv_sum += bcast64(wave_scan(ok ? t.T : 0), 63);
-        r.q_sum += bcast64(wave_scan(ok ? t.P : 0), 63);
+        r.items += wave_sum(ok ? items_of(a, t) : 0);
+        r.kv_sum += wave_sum(ok ? t.T : 0);
+        r.q_sum += wave_sum(ok ? t.P : 0);
         r.bad |= __ballot(b < a.batch && !ok) != 0;
         r.unordered |= __ballot(b < a.batch && a.cu_q[b + 1] < a.cu_q[b]) != 0;
     }
@@ -248,35 +252,97 @@ __device__ bool batch_prologue(const AttnArgs &a, int64_t &items) {
 }
 
 // The request holding work item w (or, with by_token, packed row w), with its
-// first partial row and first (KV head, row block) unit; local = w's index
+// first partial row; local = w's index
 // within the request.  Wave-uniform result.
 __device__ bool find_request(const AttnArgs &a, int64_t w, bool by_token, Seq &s, int &local) {
     const int lane = threadIdx.x & 63;
-    int64_t items = 0, part = 0, units = 0;
+    int64_t items = 0, part = 0;
     for (int b0 = 0; b0 < a.batch; b0 += 64) {
         const int b = b0 + lane;
-        Seq t;
+        Seq t{};
         const bool ok = b < a.batch && load_seq(a, b, t, false);
-        const int64_t n = ok ? items_of(a, t) : 0;
-        const int64_t pp = ok && t.ns > 1 ? (int64_t)t.ns * t.P : 0;
-        const int64_t uu = ok ? (int64_t)a.Hkv * t.rb : 0;
-        const int64_t n_in = wave_scan(n), p_in = wave_scan(pp), u_in = wave_scan(uu);
+        const int n = ok ? items_of(a, t) : 0;
+        const int pp = ok && t.ns > 1 ? sat32((int64_t)t.ns * t.P) : 0;
+        const int n_in = wave_scan(n), p_in = wave_scan(pp);
         const int64_t start = by_token ? (ok ? t.q0 : 0) : items + n_in - n;
         const int64_t len = by_token ? (ok ? t.P : 0) : n;
         const uint64_t hit = __ballot(ok && w >= start && w < start + len);
         if (hit) {
             const int src = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
             s = shfl_seq(t, src);
-            s.part_off = part + bcast64(p_in - pp, src);
-            s.unit_off = units + bcast64(u_in - uu, src);
+            s.part_off = part + bcast(p_in - pp, src);
             local = (int)(w - bcast64(start, src));
             return true;
         }
-        items += bcast64(n_in, 63);
-        part += bcast64(p_in, 63);
-        units += bcast64(u_in, 63);
+        items += bcast(n_in, 63);
+        part += bcast(p_in, 63);
     }
     return false;
+}
+
+// ---- longest-first schedule (batches of up to 64 requests).  Work is
+// grouped per (request, KV head, key split); a group's rb row blocks read
+// the same keys.  Groups are ranked by keys per group (split_len) in
+// descending order and dealt to the 8 XCDs round-robin (workgroup x runs on
+// XCD x % 8), each group's row blocks taking consecutive slots of one XCD so
+// that they share its L2.  Within an XCD workgroups start in slot order, so
+// each XCD works through its groups longest first (a greedy longest-
+// processing-time schedule): short groups fill in behind long ones instead
+// of trailing alone.  Every group has R = the batch's largest rb slots;
+// slots past a request's own rb exit at once.
+
+// Slot count of the longest-first grid: every XCD holds at most
+// ceil(groups / 8) groups of at most rbmax row blocks each.
+__host__ __device__ __forceinline__ int64_t sorted_slots(int64_t groups, int64_t rbmax) {
+    return ((groups + 7) / 8) * 8 * rbmax;
+}
+
+// The (request, KV head, split, row block) of slot x, or false for an empty
+// slot.  Requires batch <= 64 (lane j = request j).  XCD x % 8 takes every
+// 8th group of the longest-first order, and its slots are those groups'
+// row blocks, packed densely in that order.  Wave-uniform result.
+__device__ bool locate_sorted(const AttnArgs &a, int64_t x, Seq &s, int &h, int &split, int &rblk) {
+    const int lane = threadIdx.x & 63;
+    Seq t{};
+    const bool ok = lane < a.batch && load_seq(a, lane, t, false) && t.ns > 0;
+    // partial-row offsets stay in batch order (the combine kernel's order)
+    const int pp = ok && t.ns > 1 ? sat32((int64_t)t.ns * t.P) : 0;
+    const int p_excl = wave_scan(pp) - pp;
+    // rank key: keys per group descending, then request index (all distinct)
+    const uint32_t key = ok ? ((uint32_t)((1 << 24) - 1 - t.split_len) << 6) | (uint32_t)lane : 0xffffffffu;
+    const int ng = ok ? a.Hkv * t.ns : 0;                 // this request's groups
+    // groups ahead of this request in longest-first order
+    int off = 0;
+    for (int j = 0; j < a.batch; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
+        const int nj = __builtin_amdgcn_readlane(ng, j);
+        off += kj < key ? nj : 0;
+    }
+    // its groups dealt to this XCD (g in [off, off + ng), g % 8 == xcd), and
+    // the slots they take there
+    const int xcd = (int)(x & 7);
+    const int k = (int)(x >> 3);
+    auto on_xcd = [xcd](int n) { return (n + 7 - xcd) >> 3; };   // #g in [0, n) with g % 8 == xcd
+    const int slots = ok ? (on_xcd(off + ng) - on_xcd(off)) * t.rb : 0;
+    int start = 0;
+    for (int j = 0; j < a.batch; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
+        const int sj = __builtin_amdgcn_readlane(slots, j);
+        start += kj < key ? sj : 0;
+    }
+    const uint64_t hit = __ballot(slots > 0 && k >= start && k < start + slots);
+    if (!hit) return false;
+    const int b = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
+    s = shfl_seq(t, b);
+    s.part_off = bcast(p_excl, b);
+    const int kk = k - bcast(start, b);
+    const int off_b = bcast(off, b);
+    const int g = off_b + ((xcd - off_b) & 7) + 8 * (kk / s.rb);   // the (kk / rb)-th of its groups here
+    const int local = g - off_b;
+    h = local / s.ns;
+    split = local % s.ns;
+    rblk = kk % s.rb;
+    return true;
 }
 
 // Base pointers and token strides of the prefix and pack keys of one
@@ -386,20 +452,27 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     // consecutive items (the row blocks of one key split) run on one XCD
     // (workgroups are dealt to the 8 XCDs round-robin) and share its L2.
     Seq sq;
-    int local;
+    int rb, split, h;
     {
         int64_t total;
         if (!batch_prologue(a, total)) return;
-        const int64_t n8 = (total + 7) & ~(int64_t)7;
-        const int64_t x = blockIdx.x;
-        if (x >= n8) return;
-        const int64_t w = (x & 7) * (n8 >> 3) + (x >> 3);
-        if (w >= total) return;
-        if (!find_request(a, w, false, sq, local)) return;
+        if (a.batch <= 64) {
+            if (!locate_sorted(a, blockIdx.x, sq, h, split, rb)) return;
+        } else {
+            // larger batches: items in batch order, consecutive items (the
+            // row blocks of one key split) on one XCD
+            const int64_t n8 = (total + 7) & ~(int64_t)7;
+            const int64_t x = blockIdx.x;
+            if (x >= n8) return;
+            const int64_t w = (x & 7) * (n8 >> 3) + (x >> 3);
+            if (w >= total) return;
+            int local;
+            if (!find_request(a, w, false, sq, local)) return;
+            rb = local % sq.rb;
+            split = (local / sq.rb) % sq.ns;
+            h = local / (sq.rb * sq.ns);
+        }
     }
-    const int rb = local % sq.rb;
-    const int split = (local / sq.rb) % sq.ns;
-    const int h = local / (sq.rb * sq.ns);
     const int k_begin = split * sq.split_len;
     const int k_end = min(sq.T, k_begin + sq.split_len);
 
@@ -1071,7 +1144,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     const int64_t rbmax = (pmax * a.G + a.rows_wg - 1) / a.rows_wg;
     const int64_t nsplit = a.chunk == kNoSplit ? batch : ((int64_t)total_kv + a.chunk - 1) / a.chunk + batch;
     int64_t items = (int64_t)num_kv_heads * rbmax * nsplit;
-    items = (items + 7) & ~(int64_t)7;
+    items = batch <= 64 ? sorted_slots((int64_t)num_kv_heads * nsplit, rbmax) : (items + 7) & ~(int64_t)7;
     const unsigned grid = (unsigned)items;
 #define CAST_LAUNCH(DD, W)                                                 \
     (kv.store ? tree_attn_mfma_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
