@@ -19,6 +19,7 @@ oracle timed on host cores on a one-request sample, and secondary workloads
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
@@ -32,6 +33,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "tree-verify attn µs/call + % HBM roofline, Qwen3-8B shape, N=128, ctx 8k, B=8"
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_MFMA_BF16 = 2.5e15    # FLOP/s, dense bf16
+PEAK_MFMA_FP32 = 157.3e12  # FLOP/s, dense fp32
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
@@ -42,11 +44,12 @@ def log(*a):
 def roofline(wl, seconds):
     """Binding-side roofline of one attention call over ``wl``."""
     byt, flo = wl.algorithmic_bytes(), wl.algorithmic_flops()
-    t_hbm, t_mfma = byt / PEAK_HBM, flo / PEAK_MFMA_BF16
+    peak = PEAK_MFMA_FP32 if wl.dtype == "fp32" else PEAK_MFMA_BF16
+    t_hbm, t_mfma = byt / PEAK_HBM, flo / peak
     if t_mfma >= t_hbm:
         ach = flo / seconds / 1e12
-        return dict(bound="mfma", achieved=round(ach, 2), peak=PEAK_MFMA_BF16 / 1e12, unit="TFLOP/s",
-                    frac=round(ach / (PEAK_MFMA_BF16 / 1e12), 4))
+        return dict(bound="mfma", achieved=round(ach, 2), peak=peak / 1e12, unit="TFLOP/s",
+                    frac=round(ach / (peak / 1e12), 4))
     ach = byt / seconds / 1e9
     return dict(bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM / 1e9, unit="GB/s",
                 frac=round(ach / (PEAK_HBM / 1e9), 4))
@@ -246,21 +249,48 @@ def kv_append(dev, steps, warmup, layers=36):
             dst_p.append(int(wl.prefix_len[b]) + j)
     src, dst_b, dst_p = (torch.tensor(x, dtype=torch.long, device=dev) for x in (src, dst_b, dst_p))
 
-    def fused():
-        # a decode loop hands over new pack tensors every round (key[0] / value[0]
-        # of that round's forward): fresh views, so no per-tensor cache can hit
-        serving.append_accepted(buf_k, buf_v, store_len, meta["cu_q"], path, plen, [x[:] for x in pack_k],
-                                [x[:] for x in pack_v])
+    # a decode loop hands over new pack tensors every round (key[0] / value[0]
+    # of that round's forward): every call gets its own fresh views, made
+    # before the timed region, so no per-tensor cache can hit
+    rounds = [([x[:] for x in pack_k], [x[:] for x in pack_v]) for _ in range(steps + warmup)]
+    turn = [0]
+
+    def explicit():
+        pk, pv = rounds[turn[0] % len(rounds)]
+        turn[0] += 1
+        serving.append_accepted(buf_k, buf_v, store_len, meta["cu_q"], path, plen, pk, pv)
+
+    def hooked(n, w):
+        # the serving flow: the attention hook recorded each layer's pack
+        # K/V as the forward ran (serving._PACK_REC, done here before the
+        # events), and the append reads PACK_KV
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
+        for i in range(w + n):
+            pk, pv = rounds[i % len(rounds)]
+            serving.PACK_KV["k"], serving.PACK_KV["v"] = pk, pv
+            serving._PACK_REC.begin(layers)
+            for li in range(layers):
+                serving._PACK_REC.note(li, pk[li], pv[li])
+            if i >= w:
+                ev[i - w][0].record()
+            serving.append_accepted(buf_k, buf_v, store_len, meta["cu_q"], path, plen)
+            if i >= w:
+                ev[i - w][1].record()
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) * 1e3 for a, b in ev)
 
     def per_layer():
         for li in range(layers):
             buf_k[li][dst_b, :, dst_p] = pack_k[li][:, src].permute(1, 0, 2)
             buf_v[li][dst_b, :, dst_p] = pack_v[li][:, src].permute(1, 0, 2)
 
-    t_f = time_kernel(fused, steps, warmup)
+    t_f = hooked(steps, warmup)
+    t_x = time_kernel(explicit, steps, warmup)
     t_r = time_kernel(per_layer, steps, warmup)
-    log(f"  kv append ({layers} layers, {len(src)} rows): fused {t_f:.1f} us, per-layer indexing {t_r:.1f} us")
-    return dict(fused_us=round(t_f, 2), per_layer_indexing_us=round(t_r, 2), layers=layers, rows=len(src))
+    log(f"  kv append ({layers} layers, {len(src)} rows): fused {t_f:.1f} us (explicit pack lists {t_x:.1f} us), "
+        f"per-layer indexing {t_r:.1f} us")
+    return dict(fused_us=round(t_f, 2), fused_explicit_packs_us=round(t_x, 2), per_layer_indexing_us=round(t_r, 2),
+                layers=layers, rows=len(src))
 
 
 def cache_gather(dev, steps, warmup, layers=36):
@@ -344,43 +374,108 @@ def draft_trees(dev, steps, warmup):
                 topk_gbps=round(B * L * V * 2 / (t_k * 1e-6) / 1e9, 1))
 
 
+def bitmask_lines(dev, steps, warmup):
+    """K1 (ancestor words) on the headline trees (1024 rows) and on the B=32
+    stress trees (4096 rows), and K3 (greedy accept) on the headline trees
+    with full Qwen3-vocabulary bf16 logits."""
+    import torch
+    from cast_amd import greedy_accept, scenarios, tree_bitmask
+    res = {}
+    for key, wl in (("tree_bitmask", scenarios.qwen3_headline()), ("tree_bitmask_b32", scenarios.stress_mixed())):
+        meta = wl.meta_tensors(dev)
+        t_bm = time_kernel(lambda: tree_bitmask(meta["parent"], meta["cu_q"], 2), steps, warmup)
+        res[key] = dict(us_per_call=round(t_bm, 2), rows=int(wl.total_q))
+        log(f"  {key}: {t_bm:.1f} us for {wl.total_q} rows")
+    wl = scenarios.qwen3_headline()
+    meta = wl.meta_tensors(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    logits = torch.randn(wl.total_q, wl.vocab, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    tok = torch.from_numpy(wl.packed.token).to(dev)
+    t_acc = time_kernel(lambda: greedy_accept(logits, meta["cu_q"], meta["parent"], tok), steps, warmup)
+    lb = wl.total_q * wl.vocab * 2
+    res["greedy_accept"] = dict(us_per_call=round(t_acc, 2), logits_bytes=lb,
+                                hbm_frac=round(lb / (t_acc * 1e-6) / PEAK_HBM, 4))
+    log(f"  greedy_accept {t_acc:.1f} us ({lb / t_acc / 1e3:.0f} GB/s)")
+    return res
+
+
+ATTN_WORKLOADS = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
+                  "qwen3-8b-stress-b32", "qwen3-8b-b8-ctx8k-p128-fp32")
+
+
+def attn_workload(dev, name, steps, warmup):
+    """One attention workload timed like the headline (2 rotated K/V sets)."""
+    import torch
+    from cast_amd import scenarios
+    if name.endswith("-fp32"):
+        # the headline shapes in fp32: what the unchanged reference hook
+        # hands the kernel (cast_trees/serving.py:68-71)
+        wl = dataclasses.replace(scenarios.CONFIGS[name[:-5]](), dtype="fp32", name=name)
+    else:
+        wl = scenarios.CONFIGS[name]()
+    h = Harness(wl, dev, sets=2, kv_split=0)
+    t = h.time(steps, warmup)
+    rl = roofline(wl, t["attn_us"] * 1e-6)
+    res = dict(us_per_call=round(t["call_us"], 2), attn_us=round(t["attn_us"], 2),
+               combine_us=round(t["combine_us"], 2), dtype=wl.dtype, bound=rl["bound"], frac=rl["frac"],
+               hbm_frac=round(wl.algorithmic_bytes() / (t["call_us"] * 1e-6) / PEAK_HBM, 4),
+               tokens=int(wl.total_q), kv_tokens=int(wl.total_kv), kv_split=h.plan.kv_split,
+               algorithmic_bytes=wl.algorithmic_bytes(), algorithmic_flops=wl.algorithmic_flops())
+    log(f"  {name}: {t['call_us']:.1f} us/call (attn {t['attn_us']:.1f}, combine {t['combine_us']:.1f}), "
+        f"{rl['bound']} frac {rl['frac']:.3f}")
+    del h
+    torch.cuda.empty_cache()
+    return res
+
+
 def secondary(dev, steps, warmup):
     import torch
     from cast_amd import greedy_accept, scenarios, tree_bitmask
     res = {}
-    for name in ("qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128", "qwen3-8b-stress-b32"):
-        wl = scenarios.CONFIGS[name]()
-        h = Harness(wl, dev, sets=2, kv_split=0)
-        t = h.time(steps, warmup)
-        rl = roofline(wl, t["attn_us"] * 1e-6)
-        res[name] = dict(us_per_call=round(t["call_us"], 2), attn_us=round(t["attn_us"], 2),
-                         combine_us=round(t["combine_us"], 2), bound=rl["bound"], frac=rl["frac"],
-                         hbm_frac=round(wl.algorithmic_bytes() / (t["call_us"] * 1e-6) / PEAK_HBM, 4),
-                         tokens=int(wl.total_q), kv_tokens=int(wl.total_kv))
-        log(f"  {name}: {t['call_us']:.1f} us/call (attn {t['attn_us']:.1f}, combine {t['combine_us']:.1f}), "
-            f"{rl['bound']} frac {rl['frac']:.3f}")
-        del h
-        torch.cuda.empty_cache()
+    for name in ATTN_WORKLOADS:
+        res[name] = attn_workload(dev, name, steps, warmup)
     # the store path is the headline's attention on another layout: timed with
     # the headline's step and warmup counts (fresh stores settle over ~20 calls)
     res["store_layout"] = store_layout(dev, max(steps, 60), max(warmup, 20))
     res["kv_append"] = kv_append(dev, steps, warmup)
     res["cache_gather"] = cache_gather(dev, steps, warmup)
     res["draft_trees"] = draft_trees(dev, steps, warmup)
-    # K1 and K3 on the headline trees, full Qwen3 vocabulary logits
-    wl = scenarios.qwen3_headline()
-    meta = wl.meta_tensors(dev)
-    t_bm = time_kernel(lambda: tree_bitmask(meta["parent"], meta["cu_q"], 2), steps, warmup)
-    g = torch.Generator(device=dev).manual_seed(0)
-    logits = torch.randn(wl.total_q, wl.vocab, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    tok = torch.from_numpy(wl.packed.token).to(dev)
-    t_acc = time_kernel(lambda: greedy_accept(logits, meta["cu_q"], meta["parent"], tok), steps, warmup)
-    lb = wl.total_q * wl.vocab * 2
-    res["tree_bitmask"] = dict(us_per_call=round(t_bm, 2), rows=int(wl.total_q))
-    res["greedy_accept"] = dict(us_per_call=round(t_acc, 2), logits_bytes=lb,
-                                hbm_frac=round(lb / (t_acc * 1e-6) / PEAK_HBM, 4))
-    log(f"  tree_bitmask {t_bm:.1f} us, greedy_accept {t_acc:.1f} us ({lb / t_acc / 1e3:.0f} GB/s)")
+    res.update(bitmask_lines(dev, steps, warmup))
     return res
+
+
+def clock_trace(dev, n, sets):
+    """The headline call n times from a cold start, each followed by a shader
+    clock sample (cast_clock_sample): per call the event time, the clock and
+    their product, the shader cycles per call.  Flat cycles under a moving
+    time mean the clock moved, not the kernel."""
+    import torch
+    from cast_amd import _lib, scenarios
+    lib = _lib.load()
+    wl = scenarios.qwen3_headline()
+    h = Harness(wl, dev, sets=sets, kv_split=0)
+    buf = torch.zeros(2 * n, dtype=torch.int64, device=dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(n)]
+    stream = _lib.stream_of(buf)
+    torch.cuda.synchronize()
+    for i in range(n):
+        ev[i][0].record()
+        h.call(i)
+        ev[i][1].record()
+        _lib.check(lib.cast_clock_sample(_lib.ptr(buf), i, 1000, stream), "cast_clock_sample")
+    torch.cuda.synchronize()
+    us = [a.elapsed_time(b) * 1e3 for a, b in ev]
+    cw = buf.view(n, 2).cpu().tolist()
+    ghz = [c / (w / 100.0) / 1e3 for c, w in cw]          # cycles per ns
+    mcyc = [t * f / 1e3 for t, f in zip(us, ghz)]
+    win = 10
+    windows = [dict(calls=f"{lo}-{min(lo + win, n) - 1}", us=round(statistics.median(us[lo:lo + win]), 1),
+                    ghz=round(statistics.median(ghz[lo:lo + win]), 3),
+                    mcycles=round(statistics.median(mcyc[lo:lo + win]), 4)) for lo in range(0, n, win)]
+    for w in windows:
+        log(f"  calls {w['calls']:>9s}: {w['us']:7.1f} us  {w['ghz']:.3f} GHz  {w['mcycles']:.4f} Mcycles")
+    return dict(workload=wl.name, calls=n, window=win, windows=windows,
+                per_call=[[round(t, 1), round(f, 3)] for t, f in zip(us, ghz)])
 
 
 def main():
@@ -393,8 +488,11 @@ def main():
     ap.add_argument("--kv-split", type=int, default=0, help="keys per split-K chunk (0: library choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", choices=["kv_append", "cache_gather", "draft_trees", "store_layout"],
+    ap.add_argument("--only", choices=["kv_append", "cache_gather", "draft_trees", "store_layout", "tree_bitmask",
+                                       *ATTN_WORKLOADS],
                     help="only run one secondary workload (for kernel profiles); prints its JSON")
+    ap.add_argument("--clock-trace", type=int, default=0, metavar="N",
+                    help="only run N headline calls from a cold start, each followed by a shader clock sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches), to scale HBM byte counters")
     args = ap.parse_args()
@@ -419,9 +517,15 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
         return
+    if args.clock_trace:
+        print(json.dumps({"clock_trace": clock_trace(dev, args.clock_trace, args.sets)}), flush=True)
+        return
     if args.only:
+        if args.only in ATTN_WORKLOADS:
+            print(json.dumps({args.only: attn_workload(dev, args.only, args.steps, args.warmup)}), flush=True)
+            return
         fn = {"kv_append": kv_append, "cache_gather": cache_gather, "draft_trees": draft_trees,
-              "store_layout": store_layout}[args.only]
+              "store_layout": store_layout, "tree_bitmask": bitmask_lines}[args.only]
         print(json.dumps({args.only: fn(dev, args.steps, args.warmup)}), flush=True)
         return
     log(f"device: {torch.cuda.get_device_name(dev)}")

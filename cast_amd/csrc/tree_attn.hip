@@ -424,6 +424,28 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// The unit of the calling workgroup, after the batch prologue; false when
+// the workgroup has none (or the batch was rejected).  Batches of up to 64
+// requests use the longest-first schedule; larger ones take items in batch
+// order, consecutive items (the row blocks of one key split) on one XCD
+// (workgroups are dealt to the 8 XCDs round-robin) so that they share its L2.
+__device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, int &split, int &rb) {
+    int64_t total;
+    if (!batch_prologue(a, total)) return false;
+    if (a.batch <= 64) return locate_sorted(a, blockIdx.x, sq, h, split, rb);
+    const int64_t n8 = (total + 7) & ~(int64_t)7;
+    const int64_t x = blockIdx.x;
+    if (x >= n8) return false;
+    const int64_t w = (x & 7) * (n8 >> 3) + (x >> 3);
+    if (w >= total) return false;
+    int local;
+    if (!find_request(a, w, false, sq, local)) return false;
+    rb = local % sq.rb;
+    split = (local / sq.rb) % sq.ns;
+    h = local / (sq.rb * sq.ns);
+    return true;
+}
+
 template <int D, int WAVES, bool STORE>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void tree_attn_mfma_kernel(AttnArgs a) {
@@ -448,31 +470,10 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t Vt[NBUF][D * VPAD];
     __shared__ EpiArgs epi;
 
-    // ---- which unit is this workgroup?  Work items are renumbered so that
-    // consecutive items (the row blocks of one key split) run on one XCD
-    // (workgroups are dealt to the 8 XCDs round-robin) and share its L2.
+    // ---- which unit is this workgroup?
     Seq sq;
     int rb, split, h;
-    {
-        int64_t total;
-        if (!batch_prologue(a, total)) return;
-        if (a.batch <= 64) {
-            if (!locate_sorted(a, blockIdx.x, sq, h, split, rb)) return;
-        } else {
-            // larger batches: items in batch order, consecutive items (the
-            // row blocks of one key split) on one XCD
-            const int64_t n8 = (total + 7) & ~(int64_t)7;
-            const int64_t x = blockIdx.x;
-            if (x >= n8) return;
-            const int64_t w = (x & 7) * (n8 >> 3) + (x >> 3);
-            if (w >= total) return;
-            int local;
-            if (!find_request(a, w, false, sq, local)) return;
-            rb = local % sq.rb;
-            split = (local / sq.rb) % sq.ns;
-            h = local / (sq.rb * sq.ns);
-        }
-    }
+    if (!locate_item(a, sq, h, split, rb)) return;
     const int k_begin = split * sq.split_len;
     const int k_end = min(sq.T, k_begin + sq.split_len);
 
@@ -772,6 +773,276 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     }
 }
 // --------------------------------------------------------------------------
+// MFMA kernel for fp32 inputs: head_dim D in {64, 128}, WAVES waves x 32
+// query rows, v_mfma_f32_32x32x2_f32.  The reference hook runs its kernel on
+// fp32 copies of q/k/v (cast_trees/serving.py:68-71), where p stays fp32
+// for the value product (tree_attn.py:66,87 cast p to the input dtype):
+// so does this kernel.  Same structure as the bf16 kernel: S^T = K Q^T with
+// each lane owning one query column, P^T straight from the S^T
+// accumulators, O^T += V^T P^T.  A 32x32x2 step takes one value per lane
+// per operand: in the QK product lane (l32, g) supplies head-dim element
+// (D/2)*g + step of its key and of its query, so a lane's K operands for
+// four steps are one 16-byte LDS read; in the PV product it supplies the
+// value of key 8*(e/4) + 4*g + e%4 at step e, which is exactly its own
+// accumulator element e.  V sits in LDS as V'[key][l*DB + db] =
+// V[key][32*db + l], so one read gives lane l the operands of all DB
+// output blocks.  The product is MFMA-bound (16 x the bf16 cycles per
+// flop): staging and softmax are small beside it.
+// --------------------------------------------------------------------------
+template <int D, int WAVES, bool STORE>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void tree_attn_f32_kernel(AttnArgs a) {
+    constexpr int NT = WAVES * 64;
+    constexpr int BN = 64;                 // keys per tile
+    constexpr int ROWS = WAVES * 32;       // query rows per workgroup
+    constexpr int DH = D / 2;              // k-steps per 32-key block (2 head-dim values each)
+    constexpr int DB = D / 32;             // 32-row blocks of O^T
+    constexpr int KPAD = D + 4;            // LDS row stride (floats)
+    constexpr int KCH = BN * D / 4;        // 16-byte K chunks per tile
+    constexpr int K_PER_T = (KCH + NT - 1) / NT;
+    constexpr int VUNITS = BN * 8;         // (key, group of 4 l) staging units of V
+    constexpr int V_PER_T = (VUNITS + NT - 1) / NT;
+    typedef float floatxDB __attribute__((ext_vector_type(DB)));
+
+    __shared__ __attribute__((aligned(16))) float Ks[2][BN * KPAD];
+    __shared__ __attribute__((aligned(16))) float Vs[2][BN * KPAD];
+    __shared__ EpiArgs epi;
+
+    Seq sq;
+    int rb, split, h;
+    if (!locate_item(a, sq, h, split, rb)) return;
+    const int k_begin = split * sq.split_len;
+    const int k_end = min(sq.T, k_begin + sq.split_len);
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int g = lane >> 5;
+    const int l32 = lane & 31;
+    const int rows = sq.P * a.G;
+    const int r = rb * ROWS + wave * 32 + l32;
+    const bool active = rb * ROWS + wave * 32 < rows;
+    const bool qvalid = r < rows;
+    const int qtok = sq.q0 + (qvalid ? r / a.G : 0);
+    const int qhead = h * a.G + (qvalid ? r % a.G : 0);
+    const KvView<float> kv(a.kv, sq, h);
+
+    // Q operand: head-dim elements [DH*g, DH*g + DH) of this lane's query
+    float qf[DH];
+    {
+        const float *src = static_cast<const float *>(a.q) + (int64_t)qtok * a.q_tok + (int64_t)qhead * a.q_head +
+                           DH * g;
+#pragma unroll
+        for (int i = 0; i < DH / 4; ++i) {
+            const floatx4 x = qvalid ? *reinterpret_cast<const floatx4 *>(src + 4 * i) : floatx4{};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qf[4 * i + j] = x[j];
+        }
+    }
+    uint64_t mw0 = 0, mw1 = 0;
+    if (qvalid && k_end > sq.S) {
+        const uint64_t *mp = a.mask + (int64_t)qtok * a.mask_words;
+        mw0 = mp[0];
+        if (a.mask_words > 1) mw1 = mp[1];
+    }
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = floatx16{};
+    float m = -INFINITY, msafe = 0.f, lsum = 0.f;
+    const float c = a.scale_log2;
+
+    const int pre_end = min(k_end, sq.S);
+    const int n_pre = k_begin < pre_end ? (pre_end - k_begin + BN - 1) / BN : 0;
+    const int pk_begin = max(k_begin, sq.S);
+    const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
+    const int ntiles = n_pre + n_pack;
+    auto tile_t0 = [&](int t) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
+    auto tile_valid = [&](int t) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
+
+    const uint32_t ksb_pre = (uint32_t)kv.kpre_t * 4u, vsb_pre = (uint32_t)kv.vpre_t * 4u;
+    const uint32_t ksb_pack = (uint32_t)kv.kpack_t * 4u, vsb_pack = (uint32_t)kv.vpack_t * 4u;
+    const int rows_pre = STORE ? sq.S : sq.T;
+    const __amdgpu_buffer_rsrc_t kr_pre = seg_rsrc(kv.kpre, rows_pre, ksb_pre, D * 4);
+    const __amdgpu_buffer_rsrc_t vr_pre = seg_rsrc(kv.vpre, rows_pre, vsb_pre, D * 4);
+    const __amdgpu_buffer_rsrc_t kr_pack = seg_rsrc(kv.kpack, STORE ? sq.P : 0, ksb_pack, D * 4);
+    const __amdgpu_buffer_rsrc_t vr_pack = seg_rsrc(kv.vpack, STORE ? sq.P : 0, vsb_pack, D * 4);
+    u32x4 kst[K_PER_T];
+    u32x4 vst[V_PER_T][DB];
+    auto fetch = [&](int t) {
+        const bool pre = !STORE || t < n_pre;
+        const int t0 = tile_t0(t);
+        const uint32_t row0 = (uint32_t)(pre ? t0 : t0 - sq.S);
+        const __amdgpu_buffer_rsrc_t krs = pre ? kr_pre : kr_pack;
+        const __amdgpu_buffer_rsrc_t vrs = pre ? vr_pre : vr_pack;
+        const uint32_t ksb = pre ? ksb_pre : ksb_pack;
+        const uint32_t vsb = pre ? vsb_pre : vsb_pack;
+#pragma unroll
+        for (int it = 0; it < K_PER_T; ++it) {
+            const int cidx = tid + it * NT;
+            if (cidx >= KCH) break;
+            const int key = cidx / (D / 4), dch = cidx % (D / 4);
+            kst[it] = load16(krs, __umul24(row0 + key, ksb) + dch * 16);
+        }
+#pragma unroll
+        for (int it = 0; it < V_PER_T; ++it) {
+            const int u = tid + it * NT;
+            if (u >= VUNITS) break;
+            const int key = u >> 3, lg = u & 7;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+                vst[it][db] = load16(vrs, __umul24(row0 + key, vsb) + db * 128 + lg * 16);
+        }
+    };
+    // register -> LDS: K as is; V with d = 32*db + l stored at l*DB + db
+    auto publish = [&](int buf) {
+#pragma unroll
+        for (int it = 0; it < K_PER_T; ++it) {
+            const int cidx = tid + it * NT;
+            if (cidx >= KCH) break;
+            const int key = cidx / (D / 4), dch = cidx % (D / 4);
+            *reinterpret_cast<u32x4 *>(&Ks[buf][key * KPAD + dch * 4]) = kst[it];
+        }
+#pragma unroll
+        for (int it = 0; it < V_PER_T; ++it) {
+            const int u = tid + it * NT;
+            if (u >= VUNITS) break;
+            const int key = u >> 3, lg = u & 7;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                floatxDB w;
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    // element i through a scalar: hipcc (ROCm 7.2) reads element 0
+                    // for every i of __builtin_bit_cast(float, vec[db][i])
+                    const uint32_t bits = vst[it][db][i];
+                    w[db] = __builtin_bit_cast(float, bits);
+                }
+                *reinterpret_cast<floatxDB *>(&Vs[buf][key * KPAD + (4 * lg + i) * DB]) = w;
+            }
+        }
+    };
+
+    if (tid == 0) {
+        epi.out = a.out;
+        epi.lse = a.lse;
+        epi.part_o = a.part_o;
+        epi.part_lse = a.part_lse;
+        epi.status = a.status;
+        epi.o_tok = a.o_tok;
+        epi.o_head = a.o_head;
+        epi.part_rows = a.part_rows;
+        epi.prow0 = sq.part_off + (int64_t)split * sq.P - sq.q0;
+        epi.ns = sq.ns;
+        epi.Hq = a.Hq;
+    }
+    __syncthreads();
+
+    if (ntiles > 0) fetch(0);
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        publish(buf);
+        __syncthreads();
+        if (t + 1 < ntiles) fetch(t + 1);
+        if (!active) continue;
+        // S^T = K Q^T, the two 32-key blocks' chains interleaved
+        floatx16 s[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+        for (int i = 0; i < DH / 4; ++i) {
+            const floatx4 k0 = *reinterpret_cast<const floatx4 *>(&Ks[buf][l32 * KPAD + DH * g + 4 * i]);
+            const floatx4 k1 = *reinterpret_cast<const floatx4 *>(&Ks[buf][(32 + l32) * KPAD + DH * g + 4 * i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0[j], qf[4 * i + j], s[0], 0, 0, 0);
+                s[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1[j], qf[4 * i + j], s[1], 0, 0, 0);
+            }
+        }
+        // visibility on pack tiles and partial tiles (as in the bf16 kernel)
+        const int t0 = tile_t0(t);
+        const int valid = tile_valid(t);
+        const bool pack_tile = t >= n_pre;
+        if (pack_tile || valid < BN) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int k0 = kb * 32 + 4 * g;
+                const int lim = valid - k0;
+                uint32_t vis = pack_tile ? vis_window(mw0, mw1, t0 - sq.S + k0) : ~0u;
+                vis &= lim >= 32 ? ~0u : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int off = 8 * (e >> 2) + (e & 3);
+                    s[kb][e] = (vis >> off) & 1u ? s[kb][e] : -INFINITY;
+                }
+            }
+        }
+        float lmax = s[0][0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) lmax = fmaxf(lmax, s[0][e]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) lmax = fmaxf(lmax, s[1][e]);
+        if (__any(lmax * c > m + kRescaleSlack)) {
+            const float mx = fmaxf(lmax, partner32(lmax)) * c;
+            const float mn = fmaxf(m, mx);
+            const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+            lsum *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db) o[db] *= alpha;
+            m = mn;
+            msafe = m == -INFINITY ? 0.f : m;
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                s[kb][e] = __builtin_amdgcn_exp2f(fmaf(s[kb][e], c, -msafe));
+                acc += s[kb][e];
+            }
+        lsum += acc;
+        // O^T += V^T P^T: step e of block kb is key 32*kb + 8*(e/4) + 4*g + e%4
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int key = kb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+                const floatxDB vv = *reinterpret_cast<const floatxDB *>(&Vs[buf][key * KPAD + l32 * DB]);
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[db], s[kb][e], o[db], 0, 0, 0);
+            }
+    }
+
+    if (!active) return;
+    const float ltot = lsum + partner32(lsum);
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
+    if (!qvalid) return;
+    const EpiArgs e = epi;
+    float *dst;
+    if (e.ns == 1) {
+        dst = static_cast<float *>(e.out) + (int64_t)qtok * e.o_tok + (int64_t)qhead * e.o_head;
+        if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
+    } else {
+        const int64_t prow = e.prow0 + qtok;
+        if (prow >= e.part_rows) {
+            raise_flag(e.status, CAST_FLAG_BAD_OFFSETS);
+            return;
+        }
+        dst = e.part_o + (prow * e.Hq + qhead) * D;
+        if (g == 0) e.part_lse[prow * e.Hq + qhead] = lse2;
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = db * 32 + 8 * r4 + 4 * g;
+            const floatx4 w = {o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
+                               o[db][4 * r4 + 3] * inv};
+            *reinterpret_cast<floatx4 *>(dst + d) = w;
+        }
+}
+
+// --------------------------------------------------------------------------
 // Split-K combine: one workgroup per packed token, all query heads.
 // --------------------------------------------------------------------------
 // One workgroup per (packed token, group of query heads): a.comb_groups
@@ -982,13 +1253,18 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
 // --------------------------------------------------------------------------
 // Host side
 // --------------------------------------------------------------------------
-static bool mfma_path(int32_t dtype, int32_t D) { return dtype == CAST_BF16 && (D == 64 || D == 128); }
+static bool mfma_path(int32_t dtype, int32_t D) {
+    return (dtype == CAST_BF16 || dtype == CAST_FP32) && (D == 64 || D == 128);
+}
 
 // Waves per workgroup (32 query rows each) for the largest possible pack.
-static int waves_for(int32_t total_q, int32_t G) {
+// (The fp32 kernel has no 2-wave instance: its staging registers would not
+// fit beside the Q and O operands.)
+static int waves_for(int32_t total_q, int32_t G, int32_t dtype) {
     const int pmax = total_q < kMaxPack ? total_q : kMaxPack;
     const int rows = pmax * G;
-    return rows <= 64 ? 2 : rows <= 128 ? 4 : 8;
+    const int w = rows <= 64 ? 2 : rows <= 128 ? 4 : 8;
+    return dtype == CAST_FP32 && w < 4 ? 4 : w;
 }
 
 static int32_t resolve_chunk(int32_t batch, int32_t total_q, int32_t total_kv, int32_t Hq, int32_t Hkv,
@@ -996,7 +1272,7 @@ static int32_t resolve_chunk(int32_t batch, int32_t total_q, int32_t total_kv, i
     if (!mfma_path(dtype, D) || kv_split < 0 || batch <= 0) return kNoSplit;
     if (kv_split > 0) return ((kv_split + 63) / 64) * 64;
     const int G = Hq / Hkv;
-    const int rows_wg = waves_for(total_q, G) * 32;
+    const int rows_wg = waves_for(total_q, G, dtype) * 32;
     const int64_t p_avg = (total_q + batch - 1) / batch;
     const int64_t p_est = p_avg < kMaxPack ? p_avg : kMaxPack;
     const int64_t rb = (p_est * G + rows_wg - 1) / rows_wg;
@@ -1124,7 +1400,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
     }
 
-    const int waves = waves_for(total_q, a.G);
+    const int waves = waves_for(total_q, a.G, dtype);
     a.rows_wg = waves * 32;
     a.chunk = resolve_chunk(batch, total_q, total_kv, num_q_heads, num_kv_heads, head_dim, dtype, kv_split);
     if (a.chunk != kNoSplit) {
@@ -1149,7 +1425,18 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
 #define CAST_LAUNCH(DD, W)                                                 \
     (kv.store ? tree_attn_mfma_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
               : tree_attn_mfma_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
+#define CAST_LAUNCH_F32(DD, W)                                                \
+    (kv.store ? tree_attn_f32_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
+              : tree_attn_f32_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
     if (!(stages & kStageAttn)) {
+    } else if (dtype == CAST_FP32) {
+        if (head_dim == 128) {
+            if (waves == 4) CAST_LAUNCH_F32(128, 4);
+            else CAST_LAUNCH_F32(128, 8);
+        } else {
+            if (waves == 4) CAST_LAUNCH_F32(64, 4);
+            else CAST_LAUNCH_F32(64, 8);
+        }
     } else if (head_dim == 128) {
         if (waves == 2) CAST_LAUNCH(128, 2);
         else if (waves == 4) CAST_LAUNCH(128, 4);
@@ -1160,6 +1447,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         else CAST_LAUNCH(64, 8);
     }
 #undef CAST_LAUNCH
+#undef CAST_LAUNCH_F32
     if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     if (a.chunk != kNoSplit && (stages & kStageCombine)) {
         // about 1536 workgroups (6 per CU), each with up to 256 output chunks
@@ -1167,10 +1455,14 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         int64_t g = 1536 / total_q;
         g = g < 1 ? 1 : (g > max_groups ? max_groups : g);
         a.comb_groups = (int32_t)g;
-        if (head_dim == 128)
-            tree_attn_combine_kernel<uint16_t, 128><<<(unsigned)(total_q * g), 256, 0, st>>>(a);
-        else
-            tree_attn_combine_kernel<uint16_t, 64><<<(unsigned)(total_q * g), 256, 0, st>>>(a);
+        const unsigned cg = (unsigned)(total_q * g);
+        if (dtype == CAST_FP32) {
+            if (head_dim == 128) tree_attn_combine_kernel<float, 128><<<cg, 256, 0, st>>>(a);
+            else tree_attn_combine_kernel<float, 64><<<cg, 256, 0, st>>>(a);
+        } else {
+            if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128><<<cg, 256, 0, st>>>(a);
+            else tree_attn_combine_kernel<uint16_t, 64><<<cg, 256, 0, st>>>(a);
+        }
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     }
     return CAST_OK;

@@ -42,7 +42,7 @@ import torch.nn.functional as F
 
 from .tree import MAX_PACK
 from .tree_attn import store_tree_attention
-from .verify import tree_bitmask
+from .verify import _i32_on, tree_bitmask
 
 
 class VerifyPassState:
@@ -77,6 +77,57 @@ PLAN = VerifyPassState()
 PACK_KV = {"k": [], "v": []}
 
 
+class _PackRecord:
+    """The pack K/V addresses of the current verify pass, recorded by the
+    hook as each layer's key[0] / value[0] arrives and checked then (shape,
+    strides, dtype, device and alignment alike in every layer), so that the
+    append after the forward needs no per-layer Python checks."""
+
+    def __init__(self):
+        self.begin(0)
+
+    def begin(self, layers):
+        self.k = (ctypes.c_void_p * layers)()
+        self.v = (ctypes.c_void_p * layers)()
+        self.objs = [None] * layers
+        self.sig = None
+        self.ok = True
+
+    def note(self, li, k, v):
+        if li >= len(self.objs):
+            self.ok = False
+            return
+        sig = (k.shape, k.stride(), v.shape, v.stride(), k.dtype, v.dtype, k.get_device(), v.get_device())
+        if self.sig is None:
+            self.sig = sig
+        elif sig != self.sig:
+            self.ok = False
+        kp, vp = k.data_ptr(), v.data_ptr()
+        if (kp | vp) & 15:
+            self.ok = False
+        self.k[li], self.v[li] = kp, vp
+        self.objs[li] = (k, v)
+
+    def arrays_for(self, lay, pack_k, pack_v):
+        """(k_ptrs, v_ptrs, k_strides, v_strides, total_q) when the record
+        covers exactly these per-layer tensors, else None."""
+        if not self.ok or self.sig is None or len(self.objs) != lay["L"] or len(pack_k) != lay["L"]:
+            return None
+        for (k, v), pk, pv in zip(self.objs, pack_k, pack_v):
+            if k is not pk or v is not pv:
+                return None
+        kshape, kstride, vshape, vstride, kdt, vdt, kdev, vdev = self.sig
+        Hkv, D = lay["Hkv"], lay["D"]
+        if (len(kshape) != 3 or tuple(kshape) != tuple(vshape) or kshape[0] != Hkv or kshape[2] != D
+                or kstride[2] != 1 or vstride[2] != 1 or kdt is not lay["dtype"] or vdt is not lay["dtype"]
+                or kdev != lay["dev_index"] or vdev != lay["dev_index"]):
+            return None
+        return self.k, self.v, (kstride[1], kstride[0]), (vstride[1], vstride[0]), int(kshape[1])
+
+
+_PACK_REC = _PackRecord()
+
+
 def _plain_attention(query, key, value, attention_mask, scaling):
     """A forward that is not a tree verify (prefill, ordinary decode): torch
     SDPA on HF's [1, H, n, D] layout, causal when there is no mask and more
@@ -101,6 +152,7 @@ def _varlen_attention(module, query, key, value, attention_mask, scaling=None, d
         PACK_KV["k"].append(None)
         PACK_KV["v"].append(None)
     PACK_KV["k"][li], PACK_KV["v"][li] = key[0], value[0]
+    _PACK_REC.note(li, key[0], value[0])
     buf_k, buf_v = PLAN.buf_k[li], PLAN.buf_v[li]
     q = query[0].transpose(0, 1)                          # [total_q, Hq, D] view
     dt = buf_k.dtype
@@ -169,6 +221,7 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
     words = tree_bitmask(parent_t, cu_q_t, 2)
     n_layers = len(buf_k)
     PACK_KV["k"], PACK_KV["v"] = [None] * n_layers, [None] * n_layers
+    _PACK_REC.begin(n_layers)
     PLAN.set(buf_k=buf_k, buf_v=buf_v, prefix_len=prefix_t, pack_len=pack_t, cu_q=cu_q_t,
              total_kv=int(sum(store_len)) + total_q, ancestor_mask=words, parent=parent_t, workspace=None)
     ids = torch.tensor([tok], dtype=torch.long, device=dev)
@@ -210,7 +263,8 @@ def _store_layout(buf_k, buf_v):
     if k0.stride(-1) != 1 or any(t.data_ptr() % 16 for t in tensors):
         raise ValueError("the store needs a contiguous, 16-byte aligned head dim")
     layout = dict(k=_ptr_array(buf_k), v=_ptr_array(buf_v), L=L, B=B, Hkv=Hkv, cap=cap, D=D, dtype=k0.dtype,
-                  device=k0.device, store_k=tuple(k0.stride()[:3]), store_v=tuple(buf_v[0].stride()[:3]))
+                  device=k0.device, dev_index=k0.get_device(), store_k=tuple(k0.stride()[:3]),
+                  store_v=tuple(buf_v[0].stride()[:3]))
     if len(_STORE_LAYOUTS) >= 8:
         _STORE_LAYOUTS.clear()
     _STORE_LAYOUTS[key] = (tuple(weakref.ref(t) for t in tensors), layout)
@@ -219,25 +273,31 @@ def _store_layout(buf_k, buf_v):
 
 def _pack_arrays(lay, pack_k, pack_v):
     """Check one round's pack K/V (new tensors every verify pass) against the
-    stores and return their address arrays, strides and total_q."""
+    stores and return their address arrays, strides and total_q.  One tight
+    pass over the 2L tensors: the common shape, strides, dtype and device,
+    and 16-byte aligned bases."""
     L = lay["L"]
     if len(pack_k) != L or len(pack_v) != L:
         raise ValueError("one pack K and one pack V tensor per layer")
-    p0, v0 = pack_k[0], pack_v[0]
-    Hkv, D = lay["Hkv"], lay["D"]
-    total_q = int(p0.shape[1]) if p0.dim() == 3 else -1
-    want = (Hkv, total_q, D)
-    for ps, ref in ((pack_k, p0), (pack_v, v0)):
+    Hkv, D, dt, dev = lay["Hkv"], lay["D"], lay["dtype"], lay["dev_index"]
+    out = []
+    for ps in (pack_k, pack_v):
+        ref = ps[0]
         shape, stride = ref.shape, ref.stride()
-        if tuple(shape) != want or stride[-1] != 1:
+        if len(shape) != 3 or shape[0] != Hkv or shape[2] != D or stride[2] != 1:
             raise ValueError(f"pack K/V must be [{Hkv}, total_q, {D}] with a contiguous head dim")
+        ptrs = []
         for t in ps:
-            if t.shape != shape or t.stride() != stride or t.dtype != lay["dtype"] or t.device != lay["device"]:
+            if t.shape != shape or t.stride() != stride or t.dtype is not dt or t.get_device() != dev:
                 raise ValueError("pack K/V must share shape, strides, the store's dtype and device in every layer")
-    kp, vp = _ptr_array(pack_k), _ptr_array(pack_v)
-    if any(a % 16 for a in kp) or any(a % 16 for a in vp):
-        raise ValueError("pack K/V need 16-byte aligned rows")
-    return kp, vp, (p0.stride(1), p0.stride(0)), (v0.stride(1), v0.stride(0)), total_q
+            ptrs.append(t.data_ptr())
+        if any(a & 15 for a in ptrs):
+            raise ValueError("pack K/V need 16-byte aligned rows")
+        out.append(((ctypes.c_void_p * L)(*ptrs), (stride[1], stride[0]), int(shape[1])))
+    (kp, kst, tq), (vp, vst, tq_v) = out
+    if tq_v != tq:
+        raise ValueError("pack K and V must hold the same packed tokens")
+    return kp, vp, kst, vst, tq
 
 
 def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_len, new_len, status=None):
@@ -250,10 +310,12 @@ def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_
     dev = lay["device"]
     if dev.type != "cuda":
         raise ValueError("the KV append runs on the GPU: stores and packs must be device tensors")
-    kp, vp, kp_st, vp_st, total_q = _pack_arrays(lay, pack_k, pack_v)
+    rec = _PACK_REC.arrays_for(lay, pack_k, pack_v)
+    kp, vp, kp_st, vp_st, total_q = rec if rec is not None else _pack_arrays(lay, pack_k, pack_v)
+    di = lay["dev_index"]
     for name, t in (("src_row", src_row), ("path", path), ("path_len", path_len), ("store_len", store_len),
                     ("new_len", new_len), ("status", status)):
-        if t is not None and t.device != dev:
+        if t is not None and t.get_device() != di:
             raise ValueError(f"{name} must be on the stores' device {dev}")
     n = int(src_row.shape[0])
     if n > lay["B"] or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
@@ -278,12 +340,12 @@ def append_accepted(buf_k, buf_v, store_len, cu_q, path, path_len, pack_k=None, 
     pack_k = PACK_KV["k"] if pack_k is None else pack_k
     pack_v = PACK_KV["v"] if pack_v is None else pack_v
     dev = buf_k[0].device
-    store_len = torch.as_tensor(store_len, device=dev).to(torch.int32).contiguous()
-    cu_q = torch.as_tensor(cu_q, device=dev).to(torch.int32).contiguous()
+    store_len = _i32_on(store_len, dev)
+    cu_q = _i32_on(cu_q, dev)
     new_len = torch.empty_like(store_len)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
-    _append_launch(buf_k, buf_v, pack_k, pack_v, cu_q[:-1].contiguous(), path.to(dev, torch.int32),
-                   path_len.to(dev, torch.int32).contiguous(), store_len, new_len, status)
+    _append_launch(buf_k, buf_v, pack_k, pack_v, cu_q[:-1], _i32_on(path, dev), _i32_on(path_len, dev), store_len,
+                   new_len, status)
     if check:
         from . import _lib
         _lib.raise_device_flags(status.item(), "append_accepted")

@@ -27,6 +27,13 @@ from . import _lib
 from .tree import MAX_PACK, ancestor_matrix, pack_trees
 
 
+def _i32_on(x, dev):
+    """x as a contiguous int32 tensor on dev (no copy when it already is one)."""
+    if isinstance(x, torch.Tensor) and x.dtype is torch.int32 and x.device == dev and x.is_contiguous():
+        return x
+    return torch.as_tensor(x, device=dev).to(torch.int32).contiguous()
+
+
 def tree_bitmask(parent, cu_q, words=2, *, check=False):
     """Ancestor words of every packed row, computed on the device.
 
@@ -39,8 +46,8 @@ def tree_bitmask(parent, cu_q, words=2, *, check=False):
         raise ValueError("words must be 1 or 2")
     parent = torch.as_tensor(parent)
     dev = parent.device if parent.is_cuda else torch.device("cuda", torch.cuda.current_device())
-    parent = parent.to(dev, torch.int32).contiguous()
-    cu_q = torch.as_tensor(cu_q, device=dev).to(torch.int32).contiguous()
+    parent = _i32_on(parent, dev)
+    cu_q = _i32_on(cu_q, dev)
     total_q = int(parent.shape[0])
     B = int(cu_q.shape[0]) - 1
     out = torch.empty((total_q, words), dtype=torch.int64, device=dev)

@@ -308,6 +308,16 @@ int cast_build_trees(const int64_t *top_idx, const void *top_lp, int32_t lp_dtyp
                      int32_t *parent, double *score, int32_t *n_nodes, int32_t *status,
                      cast_stream_t stream);
 
+/* ---------------------------------------------------------------------
+ * Measurement aid, no counterpart in the reference.  Samples the shader
+ * clock: writes out[2*slot] = shader cycles and out[2*slot + 1] = ticks of
+ * the constant 100 MHz counter over a fixed chain of `iters` dependent FMAs
+ * (one workgroup, stream-ordered).  cycles / ticks * 100 MHz is the shader
+ * clock at that point of the stream; bench.py uses it to separate a clock
+ * ramp from a change in cycles per call.  out: uint64 [2 * (slot + 1)].
+ * ------------------------------------------------------------------- */
+int cast_clock_sample(uint64_t *out, int32_t slot, int32_t iters, cast_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,7 +67,8 @@ def test_workspace_and_split_are_host_only(lib):
     ws = lib.cast_tree_attn_workspace_size(8, 1024, 66560, 32, 8, 128, 0, 0)
     assert ws > 0 and ws % 256 == 0
     assert lib.cast_tree_attn_workspace_size(8, 1024, 66560, 32, 8, 128, 0, -1) == 0     # no split
-    assert lib.cast_tree_attn_workspace_size(1, 16, 144, 4, 4, 64, 1, 0) == 0            # fp32 path
+    assert lib.cast_tree_attn_workspace_size(1, 16, 144, 4, 4, 64, 1, 0) > 0             # fp32 MFMA path splits too
+    assert lib.cast_tree_attn_workspace_size(1, 16, 144, 4, 4, 96, 1, 0) == 0            # generic path: no split
     assert lib.cast_tree_attn_workspace_size(8, 1024, 66560, 32, 7, 128, 0, 0) == 0      # bad ratio
 
 

@@ -153,3 +153,43 @@ def test_gather_cache_rejects_bad_keep(gpu):
     for keep in ([1, 2], [0, 0], [0, 15]):
         with pytest.raises(ValueError):
             gather_cache(cache, 10, keep)
+
+
+def test_append_from_hook_record_matches_explicit_packs(gpu):
+    # the serving flow: the attention hook records each layer's pack K/V as
+    # the forward runs, and append_accepted (pack lists from PACK_KV) uses
+    # those checked addresses; the result is the explicit-list result bit for bit
+    from cast_amd import serving
+    buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=21)
+    B, L = len(store_len), len(buf_k)
+    path = torch.full((B, 128), -1, dtype=torch.int32, device=gpu)
+    for b in range(B):
+        if len(keep[b]) > 1:
+            path[b, :len(keep[b]) - 1] = torch.tensor([k - 1 for k in keep[b][1:]], dtype=torch.int32)
+    plen = torch.tensor([len(k) - 1 for k in keep], dtype=torch.int32, device=gpu)
+    sl = torch.tensor(store_len, dtype=torch.int32, device=gpu)
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=gpu)
+    print(f"case append-hook-record: B={B} L={L}", flush=True)
+    want_k, want_v = [x.clone() for x in buf_k], [x.clone() for x in buf_v]
+    n_want = serving.append_accepted(want_k, want_v, sl, cq, path, plen, pack_k, pack_v, check=True)
+    got_k, got_v = [x.clone() for x in buf_k], [x.clone() for x in buf_v]
+    serving.PACK_KV["k"], serving.PACK_KV["v"] = list(pack_k), list(pack_v)
+    serving._PACK_REC.begin(L)
+    for li in range(L):
+        serving._PACK_REC.note(li, pack_k[li], pack_v[li])
+    assert serving._PACK_REC.arrays_for(serving._store_layout(got_k, got_v), pack_k, pack_v) is not None
+    n_got = serving.append_accepted(got_k, got_v, sl, cq, path, plen, check=True)
+    torch.cuda.synchronize()
+    assert torch.equal(n_got, n_want)
+    for a, b in zip(got_k + got_v, want_k + want_v):
+        assert torch.equal(a, b)
+    # a record of other tensors is not used: the lists are checked in full
+    serving._PACK_REC.begin(L)
+    for li in range(L):
+        serving._PACK_REC.note(li, pack_k[li][:], pack_v[li][:])
+    assert serving._PACK_REC.arrays_for(serving._store_layout(got_k, got_v), pack_k, pack_v) is None
+    bad = list(pack_k)
+    bad[1] = pack_k[1].contiguous()           # other strides than layer 0
+    serving.PACK_KV["k"] = bad
+    with pytest.raises(ValueError, match="strides"):
+        serving.append_accepted(got_k, got_v, sl, cq, path, plen)

@@ -177,3 +177,38 @@ def test_request_order_is_irrelevant(gpu):
         a0, a1 = slice(start0[b], start0[b] + lq0[b]), slice(start1[j], start1[j] + lq1[j])
         assert torch.equal(out0[a0], out1[a1]), f"request {b}"
         assert torch.equal(lse0[a0], lse1[a1]), f"request {b}"
+
+
+def _fp32(wl):
+    # the same workload with fp32 q/k/v (the reference hook's arithmetic,
+    # cast_trees/serving.py:68-71)
+    import dataclasses
+    return dataclasses.replace(wl, dtype="fp32", name=wl.name + "-fp32")
+
+
+def test_fp32_ragged_full_oracle(gpu):
+    _run_and_check(_fp32(SC.qwen3_ragged(seed=1)), gpu)
+
+
+@pytest.mark.parametrize("split", [0, 64, 448, -1])
+def test_fp32_split_variants(gpu, split):
+    wl = _fp32(SC.qwen3_ragged(seed=4, B=3, lo=100, hi=2500))
+    _run_and_check(wl, gpu, kv_split=split, label=f"fp32-ragged-split{split}")
+
+
+def test_fp32_edges_and_head_dim_64(gpu):
+    from cast_amd.tree import TreeNode
+    chain = [TreeNode(i, i + 1, i - 1, 0.0) for i in range(127)]
+    star = [TreeNode(i, 1, -1, 0.0) for i in range(127)]
+    wl = SC._make("edges-fp32", [chain, [], star, chain[:5], star[:63]], [0, 77, 1, 1999, 33],
+                  SC.QWEN3_8B, "fp32", 5, 1 / math.sqrt(128))
+    _run_and_check(wl, gpu)
+    for Hq, Hkv in [(8, 8), (16, 2)]:
+        wl = SC.random_parent_batch(seed=Hq, B=3, Hq=Hq, Hkv=Hkv, D=64, s_lo=50, s_hi=900, p_lo=1, p_hi=129,
+                                    dtype="fp32")
+        _run_and_check(wl, gpu, label=f"fp32-gqa{Hq}/{Hkv}-D64")
+
+
+def test_fp32_large_configs_sampled(gpu):
+    for wl, reqs in [(_fp32(SC.qwen3_headline()), [0, 7]), (_fp32(SC.stress_mixed()), [3, 30])]:
+        _run_and_check(wl, gpu, requests=reqs, kv_heads=[0, 5], label=wl.name)

@@ -242,3 +242,45 @@ def test_hf_batch_one_tree_hook_matches_sdpa(gpu):
     model.config._attn_implementation = "sdpa"
     b = model(ids).logits
     assert torch.equal(a, b)
+
+
+def test_bf16_hook_with_outlier_key_channels(gpu):
+    # The reference hook up-casts to fp32 because "large outlier channels in
+    # K make a bf16 dot lossy" (cast_trees/serving.py:68).  Plant such
+    # channels at the headline shapes: four of the 128 head-dim channels of
+    # K carry +-30 with a per-channel sign, Q carries 10 with the same signs,
+    # so every score gets a large common offset plus a wide spread (a peaky
+    # softmax).  The bf16 store path (fp32 accumulation, P rounded to bf16
+    # before the value product) must stay within the bf16 bar of the fp32
+    # oracle on the same bf16 inputs.
+    from cast_amd.tree_attn import store_tree_attention
+    wl = SC.qwen3_headline()
+    print(f"case outlier-k: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv}", flush=True)
+    q, k, v = wl.qkv(device=gpu)
+    g = torch.Generator(device=gpu).manual_seed(17)
+    chans = torch.tensor([3, 17, 64, 99], device=gpu)
+    sign = torch.tensor([1.0, -1.0, 1.0, -1.0], device=gpu)
+    kf, qf = k.float(), q.float()
+    kf[:, :, chans] = sign * 30.0 + 5.0 * torch.randn((k.shape[0], k.shape[1], 4), generator=g, device=gpu)
+    qf[:, :, chans] = sign * 10.0
+    k, q = kf.to(torch.bfloat16), qf.to(torch.bfloat16)
+    words = OB.chain_walk_words(wl.packed.parent, wl.cu_q)
+    mask = torch.from_numpy(words.view(np.int64).copy()).to(gpu)
+    meta = wl.meta_tensors(gpu)
+    kst, vst, kpk, vpk = _to_store(wl, q, k, v, gpu)
+    qh = q.transpose(0, 1).contiguous().transpose(0, 1)
+    out, lse = store_tree_attention(qh, kst, vst, kpk, vpk, meta["cu_q"], meta["prefix_len"], meta["pack_len"],
+                                    mask, total_kv=wl.total_kv, return_lse=True, check=True)
+    torch.cuda.synchronize()
+    reqs = [0, 3, 6]
+    ref_o, ref_l = OA.dense_tree_attention(q.float().cpu(), k.float().cpu(), v.float().cpu(), wl.cu_q, wl.cu_kv,
+                                           wl.prefix_len, wl.pack_len, words, requests=reqs, kv_heads=[0, 4, 7])
+    sel = ~torch.isnan(ref_l)
+    err_o = (out.float().cpu() - ref_o).abs()[sel]
+    err_l = (lse.cpu() - ref_l).abs()[sel]
+    # the planted channels add a common offset of ~106 to every score (LSE > 40)
+    top = ref_l[sel]
+    print(f"  lse range {top.min():.1f}..{top.max():.1f}; out max {err_o.max():.3e} mean {err_o.mean():.3e} "
+          f"lse max {err_l.max():.3e}", flush=True)
+    assert float(top.min()) > 40.0
+    assert err_o.max() <= 2e-2 and err_o.mean() <= 2e-3 and err_l.max() <= 1e-3
