@@ -142,10 +142,13 @@ __global__ __launch_bounds__(64) void draft_topk_combine_kernel(const TopkPart *
 //
 // Each thread keeps its best K rank keys (K >= k) in a fully unrolled sorted
 // list.  Only elements whose key is at least a threshold key enter the lists.
-// The threshold comes from the first batch (8 chunks per thread): the
-// smallest of the waves' best thread keys (the two best for k > 8), a bound
-// no final top-k element of the slice falls below since at least k distinct
-// elements are at or above it.  A chunk whose max is below the threshold's
+// The threshold comes from the first batch (8 chunks per thread): the k-th
+// largest of the NW * R best thread keys, R per wave (2 for k <= 8, 4 for
+// k > 8), a bound no final top-k element of the slice falls below since at
+// least k distinct elements are at or above it.  At k = 8 two per wave were
+// measured faster than four (16.3 against 17.0 us); for k > 8 four per wave
+// keep the threshold the k-th of 32 keys rather than of 16, which at k = 16
+// would be the smallest of them.  A chunk whose max is below the threshold's
 // value skips the per-element test.  The lists' entries are then compacted
 // into LDS and ranked by counting (k rounds over the list heads when more
 // than kTopkNT entries survive).

@@ -15,6 +15,7 @@ reference's heap exactly for the same (top_idx, top_lp).
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -66,6 +67,12 @@ def build_trees(top_idx, top_lp, budget, k=None, *, check=False):
         top_idx, top_lp = top_idx[None], top_lp[None]
     if top_idx.dim() != 3 or top_lp.shape != top_idx.shape:
         raise ValueError("top_idx and top_lp must both be [B, L, k] (or [L, k])")
+    if isinstance(budget, int) or not (isinstance(budget, torch.Tensor) and budget.is_cuda):
+        # budgets known on the host are checked here; a device tensor above 127
+        # is clamped by the kernel and flagged in the status word
+        b_host = np.asarray(budget.cpu() if isinstance(budget, torch.Tensor) else budget).reshape(-1)
+        if b_host.size and (b_host.min() < 0 or b_host.max() > MAX_PACK - 1):
+            raise ValueError(f"budget must be in [0, {MAX_PACK - 1}] nodes per tree (packs of up to {MAX_PACK} tokens)")
     if not (top_idx.is_cuda and top_lp.is_cuda) or top_lp.device != top_idx.device:
         raise ValueError("top_idx and top_lp must be on one GPU")
     B, L, kk = top_idx.shape

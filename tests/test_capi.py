@@ -236,3 +236,13 @@ def test_noalloc_entry_refuses_oversized_scratch_before_device_work(lib):
                                         None, None)
     assert st == _lib.ERR_SCRATCH_LIMIT
     assert b"no-allocation" in lib.cast_status_string(st)
+
+
+def test_build_trees_refuses_host_budgets_above_127():
+    import torch
+    from cast_amd.draft import build_trees
+    ti = torch.zeros((2, 15, 8), dtype=torch.int64)
+    tl = torch.zeros((2, 15, 8))
+    for bad in (128, -1, [10, 200]):
+        with pytest.raises(ValueError, match="budget must be in"):
+            build_trees(ti, tl, bad)
