@@ -6,6 +6,7 @@ process maps torch's HIP runtime and the library binds to the same one.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from pathlib import Path
 
@@ -99,8 +100,20 @@ def check(status, what):
 
 
 def stream_of(tensor):
+    """The raw HIP stream torch launches on for tensor's device (without
+    building a torch Stream object: ~0.1 us against ~2 us)."""
     import torch
-    return ctypes.c_void_p(torch.cuda.current_stream(tensor.device).cuda_stream)
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(tensor.device.index))
+
+
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def on_device(dev):
+    """A context that makes dev the current HIP device for the launches inside
+    it, switching only when another device is current."""
+    import torch
+    return _NO_SWITCH if torch.cuda.current_device() == dev.index else torch.cuda.device(dev)
 
 
 def ptr(tensor):

@@ -181,6 +181,16 @@ struct BatchTotals {
     bool unordered;    // cu_q decreases somewhere: accepted packs might overlap
 };
 
+// Adds the 64 requests b0 + lane (lane holding request b, ok when it passed
+// load_seq) to the totals.
+__device__ __forceinline__ void add_totals(BatchTotals &r, const AttnArgs &a, int b, bool ok, const Seq &t) {
+    r.items += wave_sum(ok ? items_of(a, t) : 0);
+    r.kv_sum += wave_sum(ok ? t.T : 0);
+    r.q_sum += wave_sum(ok ? t.P : 0);
+    r.bad |= __ballot(b < a.batch && !ok) != 0;
+    r.unordered |= __ballot(b < a.batch && a.cu_q[b + 1] < a.cu_q[b]) != 0;
+}
+
 __device__ BatchTotals batch_totals(const AttnArgs &a) {
     const int lane = threadIdx.x & 63;
     BatchTotals r{0, 0, 0, false, false};
@@ -188,11 +198,7 @@ __device__ BatchTotals batch_totals(const AttnArgs &a) {
         const int b = b0 + lane;
         Seq t{};
         const bool ok = b < a.batch && load_seq(a, b, t, threadIdx.x < 64);
-        r.items += wave_sum(ok ? items_of(a, t) : 0);
-        r.kv_sum += wave_sum(ok ? t.T : 0);
-        r.q_sum += wave_sum(ok ? t.P : 0);
-        r.bad |= __ballot(b < a.batch && !ok) != 0;
-        r.unordered |= __ballot(b < a.batch && a.cu_q[b + 1] < a.cu_q[b]) != 0;
+        add_totals(r, a, b, ok, t);
     }
     return r;
 }
@@ -243,11 +249,9 @@ __device__ void fill_unowned_rows(const AttnArgs &a, bool batch_ok) {
 
 // The start of every attention kernel: the batch totals, the fill of
 // unowned rows when needed; false when the batch is rejected whole.
-__device__ bool batch_prologue(const AttnArgs &a, int64_t &items) {
-    const BatchTotals t = batch_totals(a);
+__device__ bool batch_prologue(const AttnArgs &a, const BatchTotals &t) {
     const bool ok = batch_fits(a, t);
     if (!ok || t.bad || t.q_sum != a.total_q) fill_unowned_rows(a, ok);
-    items = t.items;
     return ok;
 }
 
@@ -298,13 +302,14 @@ __host__ __device__ __forceinline__ int64_t sorted_slots(int64_t groups, int64_t
 }
 
 // The (request, KV head, split, row block) of slot x, or false for an empty
-// slot.  Requires batch <= 64 (lane j = request j).  XCD x % 8 takes every
-// 8th group of the longest-first order, and its slots are those groups'
-// row blocks, packed densely in that order.  Wave-uniform result.
-__device__ bool locate_sorted(const AttnArgs &a, int64_t x, Seq &s, int &h, int &split, int &rblk) {
+// slot.  Requires batch <= 64: lane j holds request j (t, and loaded when it
+// passed load_seq).  XCD x % 8 takes every 8th group of the longest-first
+// order, and its slots are those groups' row blocks, packed densely in that
+// order.  Wave-uniform result.
+__device__ bool locate_sorted(const AttnArgs &a, int64_t x, const Seq &t, bool loaded, Seq &s, int &h, int &split,
+                              int &rblk) {
     const int lane = threadIdx.x & 63;
-    Seq t{};
-    const bool ok = lane < a.batch && load_seq(a, lane, t, false) && t.ns > 0;
+    const bool ok = loaded && t.ns > 0;
     // partial-row offsets stay in batch order (the combine kernel's order)
     const int pp = ok && t.ns > 1 ? sat32((int64_t)t.ns * t.P) : 0;
     const int p_excl = wave_scan(pp) - pp;
@@ -430,9 +435,19 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 // order, consecutive items (the row blocks of one key split) on one XCD
 // (workgroups are dealt to the 8 XCDs round-robin) so that they share its L2.
 __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, int &split, int &rb) {
-    int64_t total;
-    if (!batch_prologue(a, total)) return false;
-    if (a.batch <= 64) return locate_sorted(a, blockIdx.x, sq, h, split, rb);
+    if (a.batch <= 64) {
+        // one round of metadata loads serves the totals and the schedule
+        const int lane = threadIdx.x & 63;
+        Seq t{};
+        const bool ok = lane < a.batch && load_seq(a, lane, t, threadIdx.x < 64);
+        BatchTotals tot{0, 0, 0, false, false};
+        add_totals(tot, a, lane, ok, t);
+        if (!batch_prologue(a, tot)) return false;
+        return locate_sorted(a, blockIdx.x, t, ok, sq, h, split, rb);
+    }
+    const BatchTotals tot = batch_totals(a);
+    if (!batch_prologue(a, tot)) return false;
+    const int64_t total = tot.items;
     const int64_t n8 = (total + 7) & ~(int64_t)7;
     const int64_t x = blockIdx.x;
     if (x >= n8) return false;
@@ -1165,11 +1180,8 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
     // items: (b, h, 16-row block); rows_wg == 16 for this kernel
     Seq sq;
     int local;
-    {
-        int64_t total;
-        if (!batch_prologue(a, total)) return;
-        if (!find_request(a, blockIdx.x, false, sq, local)) return;
-    }
+    if (!batch_prologue(a, batch_totals(a))) return;
+    if (!find_request(a, blockIdx.x, false, sq, local)) return;
     const int rb = local % sq.rb;
     const int h = local / (sq.rb * sq.ns);
     const int rows = sq.P * a.G;

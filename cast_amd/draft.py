@@ -45,7 +45,7 @@ def topk_marginals(d_logits, k, *, on_device=False, splits=0):
     lp = torch.empty((rows, k), dtype=torch.float32, device=x.device)
     ws_bytes = lib.cast_draft_topk_workspace_size(rows, V, dt, k, int(splits)) if 1 <= k <= 16 else 0
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         st = lib.cast_draft_topk(_lib.ptr(x), x.stride(0), rows, V, dt, k, _lib.ptr(idx), _lib.ptr(lp),
                                  int(splits), _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
     _lib.check(st, "cast_draft_topk")
@@ -97,7 +97,7 @@ def build_trees(top_idx, top_lp, budget, k=None, *, check=False):
     score = torch.empty((B, n), dtype=torch.float64, device=dev)
     n_nodes = torch.empty(B, dtype=torch.int32, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.cast_build_trees(_lib.ptr(ti), _lib.ptr(tl), _lib.FP64 if tl.dtype == torch.float64 else _lib.FP32,
                                   B, L, k, _lib.ptr(budget), _lib.ptr(token),
                                   _lib.ptr(depth), _lib.ptr(parent), _lib.ptr(score), _lib.ptr(n_nodes),

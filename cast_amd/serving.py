@@ -320,7 +320,7 @@ def _append_launch(buf_k, buf_v, pack_k, pack_v, src_row, path, path_len, store_
     n = int(src_row.shape[0])
     if n > lay["B"] or path.dim() != 2 or path.shape[0] < n or path.shape[1] < MAX_PACK:
         raise ValueError("path must be [B, >=128] (as written by greedy_accept) for B <= the store batch")
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.cast_store_append(
             kp, vp, lay["k"], lay["v"], lay["L"], _lib.ptr(src_row), _lib.ptr(path), path.stride(0),
             _lib.ptr(path_len), _lib.ptr(store_len), _lib.ptr(new_len), n, total_q, lay["cap"], lay["Hkv"],

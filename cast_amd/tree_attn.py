@@ -183,7 +183,7 @@ def varlen_tree_attention(q, k, v, cu_q, cu_kv, prefix_len, pack_len, ancestor_m
             q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
             out.stride(0), out.stride(1), dt, float(sm_scale), int(kv_split),
             _lib.ptr(workspace) if ws_bytes else None, ws_bytes, _lib.ptr(status), _lib.stream_of(q))
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         if _stage_hook is None:
             _lib.check(lib.cast_tree_attn_fwd(*args), "cast_tree_attn_fwd")
         else:
@@ -262,7 +262,7 @@ def store_tree_attention(q, k_store, v_store, k_pack, v_pack, cu_q, prefix_len, 
     if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.cast_tree_attn_store_fwd(
             _lib.ptr(q), _lib.ptr(k_store), _lib.ptr(v_store), _lib.ptr(k_pack), _lib.ptr(v_pack), _lib.ptr(out),
             _lib.ptr(lse), _lib.ptr(cu_q), _lib.ptr(prefix_len), _lib.ptr(pack_len), _lib.ptr(mask), words,

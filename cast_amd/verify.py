@@ -52,7 +52,7 @@ def tree_bitmask(parent, cu_q, words=2, *, check=False):
     B = int(cu_q.shape[0]) - 1
     out = torch.empty((total_q, words), dtype=torch.int64, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.cast_tree_bitmask(_lib.ptr(parent), _lib.ptr(cu_q), B, total_q, words, _lib.ptr(out),
                                    _lib.ptr(status), _lib.stream_of(parent))
     _lib.check(st, "cast_tree_bitmask")
@@ -93,7 +93,7 @@ def greedy_accept(logits, cu_q, parent, token, *, check=False):
     argmax = torch.empty(total_q, dtype=torch.int32, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
     dt = _lib.BF16 if logits.dtype == torch.bfloat16 else _lib.FP32
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = lib.cast_greedy_accept(_lib.ptr(logits), logits.stride(0), V, dt, _lib.ptr(cu_q), _lib.ptr(parent),
                                     _lib.ptr(token), B, total_q, _lib.ptr(argmax), _lib.ptr(path),
                                     _lib.ptr(path_len), _lib.ptr(bonus), _lib.ptr(status), _lib.stream_of(logits))
@@ -231,7 +231,7 @@ def gather_cache(cache, n_prefix, keep):
         meta[:4] = (0, n - 1, n_prefix, 0)
         meta[4:4 + n - 1] = [x - 1 for x in keep[1:]]
         d32 = torch.from_numpy(meta).to(k0.device)
-        with torch.cuda.device(k0.device):
+        with _lib.on_device(k0.device):
             st = lib.cast_store_append(
                 ptrs([a + step for a in addrs[:L]]), ptrs([a + step for a in addrs[L:]]), ptrs(addrs[:L]),
                 ptrs(addrs[L:]), L, _lib.ptr(d32[0:1]), _lib.ptr(d32[4:]), MAX_PACK,
