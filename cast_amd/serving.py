@@ -231,7 +231,7 @@ def begin_verify(buf_k, buf_v, store_len, roots, trees, seq_lens, device=None):
 
 # ---- accepted-path KV append (cast_trees/serving.py:264-289)
 
-_STORE_LAYOUTS = {}   # (id, address) of every per-layer store tensor -> (weakrefs, checked layout)
+_STORE_LAYOUTS = {}   # (id and address of layer 0's K store, layers) -> (weakrefs, addresses, checked layout)
 
 
 def _ptr_array(tensors):
@@ -249,10 +249,11 @@ def _store_layout(buf_k, buf_v):
     if len(buf_v) != L or L == 0:
         raise ValueError("one K and one V store per layer")
     tensors = (*buf_k, *buf_v)
-    key = tuple((id(t), t.data_ptr()) for t in tensors)
+    addrs = [t.data_ptr() for t in tensors]
+    key = (id(buf_k[0]), addrs[0], L)
     hit = _STORE_LAYOUTS.get(key)
-    if hit is not None and all(r() is t for r, t in zip(hit[0], tensors)):
-        return hit[1]
+    if hit is not None and hit[1] == addrs and all(r() is t for r, t in zip(hit[0], tensors)):
+        return hit[2]
     k0 = buf_k[0]
     B, Hkv, cap, D = (int(x) for x in k0.shape)
     for t in tensors:
@@ -267,7 +268,7 @@ def _store_layout(buf_k, buf_v):
                   store_v=tuple(buf_v[0].stride()[:3]))
     if len(_STORE_LAYOUTS) >= 8:
         _STORE_LAYOUTS.clear()
-    _STORE_LAYOUTS[key] = (tuple(weakref.ref(t) for t in tensors), layout)
+    _STORE_LAYOUTS[key] = (tuple(weakref.ref(t) for t in tensors), addrs, layout)
     return layout
 
 
