@@ -8,7 +8,9 @@
 // Two kernels on the caller's stream:
 //   row_argmax   one workgroup per packed row: first index of the row
 //                maximum, NaN counting as the maximum (torch.argmax rule).
-//                Streams the logits once with 16-byte loads (HBM-bound).
+//                Streams the logits once with 16-byte loads.  bf16 rows
+//                compare 16-bit order keys two at a time (see below), a row
+//                holding a NaN takes the exact element-by-element scan.
 //   tree_walk    one wave per request: starting at the root row, finds the
 //                first child (lowest pack index, i.e. node order) whose draft
 //                token equals the row's argmax with one ballot per level,
@@ -28,17 +30,16 @@ __device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
     return v1 > v2 || (v1 == v2 && i1 < i2);
 }
 
+// The first index of the maximum of one row (base, vocab elements), NaN
+// counting as the maximum, element by element; the workgroup's 256 threads
+// call it together and thread 0 writes *out.
 template <bool BF16>
-__global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict__ logits, int64_t ld,
-                                                         int32_t vocab, int32_t *__restrict__ argmax) {
+__device__ void argmax_exact(const char *__restrict__ base, int32_t vocab, int32_t *__restrict__ out) {
     constexpr int NT = 256;
     constexpr int EPC = BF16 ? 8 : 4;   // elements per 16-byte chunk
-    const int row = blockIdx.x;
     const int tid = threadIdx.x;
     float best = -INFINITY;
     int bi = INT_MAX;
-    const size_t esz = BF16 ? 2 : 4;
-    const char *base = static_cast<const char *>(logits) + (size_t)row * (size_t)ld * esz;
     const bool vec = ((reinterpret_cast<uintptr_t>(base) & 15) == 0);
     const int nch = vec ? vocab / EPC : 0;
     // A thread visits its elements in increasing index order, so an element
@@ -118,6 +119,135 @@ __global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict_
         for (int w = 1; w < NT / 64; ++w)
             if (better(sv[w], si[w], best, bi)) {
                 best = sv[w];
+                bi = si[w];
+            }
+        *out = bi;
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict__ logits, int64_t ld,
+                                                         int32_t vocab, int32_t *__restrict__ argmax) {
+    const char *base = static_cast<const char *>(logits) + (size_t)blockIdx.x * (size_t)ld * (BF16 ? 2 : 4);
+    argmax_exact<BF16>(base, vocab, argmax + blockIdx.x);
+}
+
+// ---- bf16 rows by order keys.  A bf16 value with magnitude bits m (sign
+// cleared) gets the 16-bit two's-complement key m when non-negative and -m
+// when negative.  Keys order exactly as the values do for every non-NaN
+// pair, and -0 and +0 share key 0, so equal values tie as the float compare
+// has them.  A NaN has m > 0x7f80 (the magnitude of infinity); a row that
+// holds one is left to the exact scan, since NaN outranks every value there.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// The keys of the two bf16 values of one dword, and their magnitudes.  With
+// s = -1 for a negative half (0 otherwise), (bits ^ (s & 0x7fff)) - s is m
+// for a non-negative value and 0x8000 | (0x7fff - m), plus one, = -m mod 2^16
+// for a negative one: no select needed.
+__device__ __forceinline__ s16x2 bf16x2_key(uint32_t bits, u16x2 &mag) {
+    mag = __builtin_bit_cast(u16x2, bits & 0x7fff7fffu);
+    const s16x2 sv = __builtin_bit_cast(s16x2, bits) >> (short)15;
+    const uint32_t x = bits ^ (__builtin_bit_cast(uint32_t, sv) & 0x7fff7fffu);
+    return __builtin_bit_cast(s16x2, x) - sv;
+}
+__device__ __forceinline__ int bf16_key(uint16_t bits) {
+    const int m = bits & 0x7fff;
+    return (bits & 0x8000) ? -m : m;
+}
+
+// Per thread: the largest key of its 16-byte chunks (visited in increasing
+// order) and the first chunk holding it; then that chunk alone is read
+// again for the first element with the key.  Per element the scan costs
+// about three VALU operations against about nine for the float compare.
+__global__ __launch_bounds__(256) void row_argmax_bf16_kernel(const void *__restrict__ logits, int64_t ld,
+                                                              int32_t vocab, int32_t *__restrict__ argmax) {
+    constexpr int NT = 256;
+    constexpr int EPC = 8;
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const char *base = static_cast<const char *>(logits) + (size_t)row * (size_t)ld * 2;
+    const bool vec = ((reinterpret_cast<uintptr_t>(base) & 15) == 0);
+    const int nch = vec ? vocab / EPC : 0;
+    int bk = INT_MIN, bc = -1;          // best chunk key, first chunk holding it
+    u16x2 magmax = {0, 0};
+    auto chunk_key = [&](const u32x4 &w) {
+        u16x2 m0, m1, m2, m3;
+        const s16x2 k0 = bf16x2_key(w[0], m0), k1 = bf16x2_key(w[1], m1);
+        const s16x2 k2 = bf16x2_key(w[2], m2), k3 = bf16x2_key(w[3], m3);
+        magmax = __builtin_elementwise_max(magmax, __builtin_elementwise_max(__builtin_elementwise_max(m0, m1),
+                                                                             __builtin_elementwise_max(m2, m3)));
+        const s16x2 k = __builtin_elementwise_max(__builtin_elementwise_max(k0, k1), __builtin_elementwise_max(k2, k3));
+        return max((int)k[0], (int)k[1]);
+    };
+    auto visit = [&](const u32x4 &w, int c) {
+        const int k = chunk_key(w);
+        if (k > bk) {
+            bk = k;
+            bc = c;
+        }
+    };
+    // 8 chunks in flight per thread: 32 KB per workgroup, enough bytes in
+    // flight to cover the memory latency at the four workgroups per CU of a
+    // 1024-row launch
+    constexpr int UNR = 8;
+    int c = tid;
+    for (; c + (UNR - 1) * NT < nch; c += UNR * NT) {
+        u32x4 w[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) w[u] = *reinterpret_cast<const u32x4 *>(base + (size_t)(c + u * NT) * 16);
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) visit(w[u], c + u * NT);
+    }
+    for (; c < nch; c += NT) visit(*reinterpret_cast<const u32x4 *>(base + (size_t)c * 16), c);
+    // the thread's first element holding bk: inside chunk bc
+    int bi = INT_MAX;
+    if (bc >= 0) {
+        const u32x4 w = *reinterpret_cast<const u32x4 *>(base + (size_t)bc * 16);
+#pragma unroll
+        for (int e = EPC - 1; e >= 0; --e) {
+            const uint32_t bits = w[e >> 1];
+            if (bf16_key((uint16_t)(bits >> ((e & 1) * 16))) == bk) bi = bc * EPC + e;
+        }
+    }
+    // elements past the last whole chunk (or all of an unaligned row): their
+    // indices follow every chunk's, so they win only on a larger key
+    for (int i = nch * EPC + tid; i < vocab; i += NT) {
+        const uint16_t bits = reinterpret_cast<const uint16_t *>(base)[i];
+        const int m = bits & 0x7fff;
+        magmax[0] = max(magmax[0], (unsigned short)m);
+        const int k = bf16_key(bits);
+        if (k > bk || bi == INT_MAX) {
+            bk = k;
+            bi = i;
+        }
+    }
+    const bool nan = max(magmax[0], magmax[1]) > 0x7f80;
+    if (__syncthreads_or(nan)) {
+        argmax_exact<true>(base, vocab, argmax + row);
+        return;
+    }
+    // (key desc, index asc) over the workgroup
+    auto wins = [](int k1, int i1, int k2, int i2) { return k1 > k2 || (k1 == k2 && i1 < i2); };
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const int ok = __shfl_xor(bk, off);
+        const int oi = __shfl_xor(bi, off);
+        if (wins(ok, oi, bk, bi)) {
+            bk = ok;
+            bi = oi;
+        }
+    }
+    __shared__ int sk[NT / 64], si[NT / 64];
+    if ((tid & 63) == 0) {
+        sk[tid >> 6] = bk;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NT / 64; ++w)
+            if (wins(sk[w], si[w], bk, bi)) {
+                bk = sk[w];
                 bi = si[w];
             }
         argmax[row] = bi;
@@ -208,7 +338,7 @@ extern "C" int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (total_q > 0) {
         if (dtype == CAST_BF16)
-            row_argmax_kernel<true><<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
+            row_argmax_bf16_kernel<<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
         else
             row_argmax_kernel<false><<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;

@@ -115,3 +115,56 @@ def test_walk_tree_drop_in(gpu):
         assert walk_tree(wl.trees[b], padded[b].to(gpu)) == want[b]
     with pytest.raises(NotImplementedError):
         walk_tree(wl.trees[0], padded[0].to(gpu), temperature=1.0)
+
+
+def _argmax_rows(gpu, logits_dev):
+    """greedy_accept's per-row argmax over a one-request chain batch."""
+    from cast_amd import greedy_accept
+    R = logits_dev.shape[0]
+    cu_q = torch.tensor([0, R], dtype=torch.int32, device=gpu)
+    parent = torch.arange(-1, R - 1, dtype=torch.int32, device=gpu)
+    token = torch.zeros(R, dtype=torch.int64, device=gpu)
+    _, _, _, am = greedy_accept(logits_dev, cu_q, parent, token, check=True)
+    return am.cpu().numpy()
+
+
+def _bf16_bits(bits):
+    return torch.tensor([bits - 65536 if bits >= 32768 else bits], dtype=torch.int16).view(torch.bfloat16)[0]
+
+
+@pytest.mark.parametrize("V", [151936, 1001, 64])
+def test_bf16_argmax_edge_rows(gpu, V):
+    # the bf16 row scan compares 16-bit order keys: signed zeros, infinities,
+    # denormals, NaNs of either sign, ties inside a 16-byte chunk and across
+    # threads, the last element, rows whose start is not 16-byte aligned
+    g = torch.Generator().manual_seed(V)
+    rows = []
+    def row(fill):
+        return torch.full((V,), fill, dtype=torch.bfloat16)
+    r = row(-0.0); r[V // 2] = 0.0; rows.append(r)                         # +0 ties -0: index 0
+    rows.append(-(torch.rand(V, generator=g) + 0.5).bfloat16())            # negative only
+    r = torch.randn(V, generator=g).bfloat16(); r[V // 3] = float("inf"); r[V // 5] = float("inf"); rows.append(r)
+    r = row(float("-inf")); r[V - 7] = -1e30; rows.append(r)
+    rows.append(row(float("-inf")))                                        # all -inf: index 0
+    r = torch.zeros(V, dtype=torch.int16)
+    r[:] = torch.randint(1, 120, (V,), generator=g, dtype=torch.int16)     # positive denormals
+    r[V - 3] = 127
+    rows.append(r.view(torch.bfloat16))
+    r = torch.randn(V, generator=g).bfloat16(); r[V // 2] = float("nan"); r[3] = 1e30; rows.append(r)
+    r = torch.randn(V, generator=g).bfloat16(); r[V // 4] = _bf16_bits(0xFFC0); rows.append(r)   # negative NaN
+    r = torch.randn(V, generator=g).bfloat16(); r[2 * V // 3] = _bf16_bits(0xFF81); r[V // 3] = float("nan")
+    rows.append(r)
+    r = torch.randn(V, generator=g).bfloat16(); r[min(17, V - 1)] = 7.0; r[min(16, V - 1)] = 7.0
+    r[V - 1] = 7.0; rows.append(r)                                         # ties: first index
+    r = torch.randn(V, generator=g).bfloat16(); r[V - 1] = 9.0; rows.append(r)   # the last element
+    r = torch.randint(-2, 3, (V,), generator=g).bfloat16(); rows.append(r)       # many ties everywhere
+    r = torch.randn(V, generator=g).bfloat16(); r[::2] = -r[::2]; rows.append(r)
+    logits = torch.stack(rows)
+    print(f"case bf16-argmax-edges V={V}: {logits.shape[0]} rows", flush=True)
+    want = OW.row_argmax_all(logits)
+    assert np.array_equal(_argmax_rows(gpu, logits.to(gpu)), want)
+    # rows at a 2-byte (not 16-byte) aligned stride
+    wide = torch.cat([logits, logits[:, :3]], dim=1)
+    dev = wide.to(gpu)[:, :V]
+    assert dev.stride(0) == V + 3
+    assert np.array_equal(_argmax_rows(gpu, dev), want)
