@@ -106,6 +106,16 @@ def test_gqa_ratios_and_head_dim_64(gpu):
         _run_and_check(wl, gpu, label=f"gqa{Hq}/{Hkv}-D{D}-{dt}")
 
 
+@pytest.mark.parametrize("B,dtype,kv_split", [(64, "bf16", 0), (65, "bf16", 0), (65, "bf16", 192),
+                                               (130, "bf16", 0), (130, "fp32", 256)])
+def test_batches_across_the_64_request_boundary(gpu, B, dtype, kv_split):
+    # up to 64 requests: the longest-first schedule (one wave lane per
+    # request); more: items in batch order, the metadata walked 64 at a time
+    wl = SC.random_parent_batch(seed=B, B=B, Hq=8, Hkv=2, D=128, s_lo=20, s_hi=700, p_lo=1, p_hi=100,
+                                dtype=dtype, qkv_scale=0.5)
+    _run_and_check(wl, gpu, kv_split=kv_split, label=f"batch{B}-{dtype}-split{kv_split}")
+
+
 def test_empty_rows_give_zero_and_minus_inf(gpu):
     from cast_amd import varlen_tree_attention
     wl = SC.random_parent_batch(seed=9, B=2, Hq=8, Hkv=2, D=128, s_lo=0, s_hi=1, p_lo=5, p_hi=6, dtype="bf16")

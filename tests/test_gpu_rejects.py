@@ -72,6 +72,25 @@ def test_pack_longer_than_one_mask_word(gpu, kv_split):
     _check(wl, q, k, v, words, out, lse, accepted=[0, 2])
 
 
+@pytest.mark.parametrize("kv_split", [0, 160])
+def test_rejects_past_the_first_64_requests(gpu, kv_split):
+    # a 70-request batch (batch-order schedule) whose request 66 is too long
+    # for one mask word: only that request's rows are zeros / -inf
+    from cast_amd import varlen_tree_attention
+    rng = np.random.default_rng(70)
+    packs = [int(x) for x in rng.integers(1, 60, size=70)]
+    packs[66] = 90
+    prefix = [int(x) for x in rng.integers(10, 400, size=70)]
+    wl, q, k, v, words = _setup(gpu, packs, prefix, seed=5)
+    print(f"case reject-past-64 split={kv_split}: B={wl.B} total_q={wl.total_q}", flush=True)
+    meta = wl.meta_tensors(gpu)
+    one_word = torch.from_numpy(words[:, 0].view(np.int64).copy()).to(gpu)
+    out, lse = _poison(torch.empty_like(q)), _poison(torch.empty(q.shape[:2], device=gpu))
+    out, lse = varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                                     one_word, return_lse=True, kv_split=kv_split, out=out)
+    _check(wl, q, k, v, words, out, lse, accepted=[b for b in range(70) if b != 66])
+
+
 def test_offsets_that_disagree(gpu):
     from cast_amd import varlen_tree_attention
     wl, q, k, v, words = _setup(gpu, [10, 40, 20], [300, 50, 700], seed=1)
