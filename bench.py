@@ -335,6 +335,42 @@ def cache_gather(dev, steps, warmup, layers=36):
                 kept=len(keep))
 
 
+def graph_replay(dev, steps, warmup, layers=36):
+    """The verify attention of one request (S=2048, P=16: launch-bound) over
+    36 layers: 36 eager calls against one replay of a HIP graph that
+    captured the same 36 calls (split-K partials and combine each)."""
+    import torch
+    from cast_amd import scenarios, tree_bitmask, varlen_tree_attention
+    from cast_amd.tree_attn import plan
+    wl = scenarios.qwen3_single()
+    meta = wl.meta_tensors(dev)
+    mask = tree_bitmask(meta["parent"], meta["cu_q"], 2)
+    q, k, v = wl.qkv(device=dev)
+    out = torch.empty_like(q)
+    p = plan(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D)
+    ws = torch.empty(max(p.workspace_bytes, 256), dtype=torch.uint8, device=dev)
+
+    def calls():
+        for _ in range(layers):
+            varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"], mask,
+                                  out=out, workspace=ws)
+
+    eager = time_kernel(calls, steps, warmup)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    replay = time_kernel(graph.replay, steps, warmup)
+    log(f"  single-request attention x {layers} layers: eager {eager:.1f} us, graph replay {replay:.1f} us")
+    return dict(layers=layers, eager_us=round(eager, 2), graph_replay_us=round(replay, 2),
+                per_layer_eager_us=round(eager / layers, 2), per_layer_graph_us=round(replay / layers, 2))
+
+
 def draft_trees(dev, steps, warmup):
     """Drafting at Qwen3-8B shapes: B=8 requests x 15 future positions x the
     151936-entry vocabulary (bf16 logits), top-8 per position, one best-first
@@ -440,6 +476,7 @@ def secondary(dev, steps, warmup):
     res["kv_append"] = kv_append(dev, steps, warmup)
     res["cache_gather"] = cache_gather(dev, steps, warmup)
     res["draft_trees"] = draft_trees(dev, steps, warmup)
+    res["graph_replay"] = graph_replay(dev, steps, warmup)
     res.update(bitmask_lines(dev, steps, warmup))
     return res
 
@@ -489,6 +526,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", choices=["kv_append", "cache_gather", "draft_trees", "store_layout", "tree_bitmask",
+                                       "graph_replay",
                                        *ATTN_WORKLOADS],
                     help="only run one secondary workload (for kernel profiles); prints its JSON")
     ap.add_argument("--clock-trace", type=int, default=0, metavar="N",
@@ -525,7 +563,7 @@ def main():
             print(json.dumps({args.only: attn_workload(dev, args.only, args.steps, args.warmup)}), flush=True)
             return
         fn = {"kv_append": kv_append, "cache_gather": cache_gather, "draft_trees": draft_trees,
-              "store_layout": store_layout, "tree_bitmask": bitmask_lines}[args.only]
+              "store_layout": store_layout, "tree_bitmask": bitmask_lines, "graph_replay": graph_replay}[args.only]
         print(json.dumps({args.only: fn(dev, args.steps, args.warmup)}), flush=True)
         return
     log(f"device: {torch.cuda.get_device_name(dev)}")

@@ -38,6 +38,9 @@ constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kRescaleSlack = 8.0f;    // log2 headroom before the O rescale
 constexpr int kCombineFast = 4;          // splits the combine loads in one round trip
+constexpr int kCombineLdsSplits = 64;    // more splits: per-head weights in LDS up to this many
+constexpr int kCombineLdsHeads = 64;     //   and this many heads per combine workgroup
+constexpr int kCombineUnroll = 8;        // partial loads in flight per thread
 // Smallest automatic split-K chunk (keys).  Short prefixes with few (request,
 // head) units split down to two 64-key tiles per workgroup: a single request
 // at S=2048, P=16 takes 24.7 us per call at 128 keys against 32.3 us at 512.
@@ -1072,12 +1075,29 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     const int h0 = (blockIdx.x % groups) * hpg;
     Seq sq;
     int i;
-    {
-        // a rejected batch was zero-filled by the attention kernel
-        const BatchTotals t = batch_totals(a);
-        if (t.kv_sum > a.total_kv || t.q_sum > a.total_q || t.unordered) return;
+    // a rejected batch was zero-filled by the attention kernel
+    auto rejected = [&](const BatchTotals &t) { return t.kv_sum > a.total_kv || t.q_sum > a.total_q || t.unordered; };
+    if (a.batch <= 64) {
+        // one round of metadata loads: the totals and the request of tok
+        const int lane = threadIdx.x & 63;
+        Seq t{};
+        const bool ok = lane < a.batch && load_seq(a, lane, t, false);
+        BatchTotals tot{0, 0, 0, false, false};
+        add_totals(tot, a, lane, ok, t);
+        if (rejected(tot)) return;
+        const int pp = ok && t.ns > 1 ? sat32((int64_t)t.ns * t.P) : 0;
+        const int p_excl = wave_scan(pp) - pp;
+        const uint64_t hit = __ballot(ok && tok >= t.q0 && tok < t.q0 + t.P);
+        if (!hit) return;
+        const int src = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
+        sq = shfl_seq(t, src);
+        sq.part_off = bcast(p_excl, src);
+        i = tok - sq.q0;
+    } else {
+        if (rejected(batch_totals(a))) return;
+        if (!find_request(a, tok, true, sq, i)) return;
     }
-    if (!find_request(a, tok, true, sq, i) || sq.ns <= 1) return;
+    if (sq.ns <= 1) return;
     if (sq.part_off + (int64_t)sq.ns * sq.P > a.part_rows) return;
     const int64_t lstride = (int64_t)sq.P * a.Hq, xstride = lstride * D;
     const int hend = min(a.Hq, h0 + hpg);
@@ -1133,6 +1153,53 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
                 }
                 finish(c, acc, M, L);
             }
+        }
+        return;
+    }
+    const int nh = hend - h0;
+    if (ns <= kCombineLdsSplits && nh <= kCombineLdsHeads) {
+        // Every split's lse of the group's heads is loaded once (one round
+        // trip) and each head's max, sum and weights computed once, in LDS;
+        // then each chunk loads its ns partials kCombineUnroll at a time.
+        // Same operations in the same order as the loop below: same bits.
+        __shared__ float wgt[kCombineLdsHeads * kCombineLdsSplits];
+        __shared__ float hm[kCombineLdsHeads], hl[kCombineLdsHeads];
+        const float *lp0 = a.part_lse + (sq.part_off + i) * a.Hq + h0;
+        for (int t = threadIdx.x; t < nh * ns; t += 256) wgt[t] = lp0[(t / ns) + (t % ns) * lstride];
+        __syncthreads();
+        if (threadIdx.x < nh) {
+            const float *l = wgt + threadIdx.x * ns;
+            float M = -INFINITY, L = 0.f;
+            for (int s = 0; s < ns; ++s) M = fmaxf(M, l[s]);
+            if (M != -INFINITY)
+                for (int s = 0; s < ns; ++s) L += exp2f(l[s] - M);
+            hm[threadIdx.x] = M;
+            hl[threadIdx.x] = L;
+        }
+        __syncthreads();
+        for (int t = threadIdx.x; t < nh * ns; t += 256) {
+            const float M = hm[t / ns];
+            wgt[t] = M == -INFINITY ? 0.f : exp2f(wgt[t] - M);
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < nc; c += 256) {
+            const int hh = c / C;
+            const float *xp = a.part_o + ((sq.part_off + i) * a.Hq + h0 + hh) * D + (c % C) * 4;
+            const float *w = wgt + hh * ns;
+            floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+            if (hm[hh] != -INFINITY) {
+                int s = 0;
+                for (; s + kCombineUnroll <= ns; s += kCombineUnroll) {
+                    floatx4 x[kCombineUnroll];
+#pragma unroll
+                    for (int u = 0; u < kCombineUnroll; ++u)
+                        x[u] = *reinterpret_cast<const floatx4 *>(xp + (s + u) * xstride);
+#pragma unroll
+                    for (int u = 0; u < kCombineUnroll; ++u) acc += w[s + u] * x[u];
+                }
+                for (; s < ns; ++s) acc += w[s] * *reinterpret_cast<const floatx4 *>(xp + s * xstride);
+            }
+            finish(c, acc, hm[hh], hl[hh]);
         }
         return;
     }

@@ -116,6 +116,14 @@ def test_batches_across_the_64_request_boundary(gpu, B, dtype, kv_split):
     _run_and_check(wl, gpu, kv_split=kv_split, label=f"batch{B}-{dtype}-split{kv_split}")
 
 
+@pytest.mark.parametrize("kv_split", [192, 128])
+def test_many_splits_both_combine_paths(gpu, kv_split):
+    # 8320 keys per request: 44 splits (per-head weights staged in LDS) and
+    # 65 splits (the per-chunk loop for more than 64 splits)
+    _run_and_check(SC.qwen3_headline(), gpu, requests=[3], kv_heads=[0, 5], kv_split=kv_split,
+                   label=f"headline-split{kv_split}")
+
+
 def test_empty_rows_give_zero_and_minus_inf(gpu):
     from cast_amd import varlen_tree_attention
     wl = SC.random_parent_batch(seed=9, B=2, Hq=8, Hkv=2, D=128, s_lo=0, s_hi=1, p_lo=5, p_hi=6, dtype="bf16")
