@@ -1,8 +1,8 @@
 """CPU oracle for the tree-verification path.  TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
-may import this package, and only as the checker (or, for the baseline, as
-the thing timed on host cores).  The product path in ``cast_amd`` never
+may import this package, and only to check results against (or, for the
+baseline, as the thing timed on host cores).  The product path in ``cast_amd`` never
 imports it and fails loudly when its HIP library is missing.
 
 Contents, each restating the reference algorithm it cites:
