@@ -1,4 +1,4 @@
-// K4: accepted-path KV append into the per-request store, all layers in one
+// K4: accepted-path KV append into the per-request store, up to 64 layers per
 // launch.
 //
 // Replaces the per-layer scatter of cast_trees/serving.py:264-289

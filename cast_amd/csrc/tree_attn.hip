@@ -15,13 +15,17 @@
 //   the N side, so each lane ends up owning one query column), then
 //   O^T += V^T P^T with the same instruction, P^T taken straight from the
 //   S^T accumulator registers (a lane's 16 score values are exactly the 8+8
-//   k-slots it must supply), V^T read from a transposed LDS copy.
+//   k-slots it must supply), V^T read from a transposed LDS copy.  fp32
+//   inputs run the same structure on v_mfma_f32_32x32x2_f32
+//   (tree_attn_f32_kernel); other head dims take a scalar kernel.
 // K/V tiles of 64 keys are double-buffered through LDS with 16-byte loads;
 // the ancestor words are only consulted on the tile(s) holding pack keys.
 // The online softmax works in base 2 with a lazy rescale: the running max
 // moves only when a tile raises it by more than 2^8, so most tiles skip the
-// O rescale.  Long prefixes are split over keys; a combine kernel merges the
-// per-split (O, lse) pairs by log-sum-exp.
+// O rescale.  Every workgroup decodes its unit from the device-side metadata
+// (batches of up to 64 requests: longest key splits first, per XCD).  Long
+// prefixes are split over keys; a combine kernel merges the per-split
+// (O, lse) pairs by log-sum-exp.
 #include <limits.h>
 #include <math.h>
 
