@@ -9,6 +9,9 @@ positional signature, argument meaning and result, with these additions
   check       synchronise once and raise ValueError if the kernels flagged
               inconsistent metadata (off by default: the call never syncs)
   out         preallocated output [total_q, Hq, D]
+  workspace   preallocated split-K scratch (uint8 device tensor of at least
+              plan(...).workspace_bytes); one is allocated when missing
+              or too small.  Calls that share a workspace must not overlap.
 
 Each request b owns query rows [cu_q[b], cu_q[b+1]) (its pack of
 P_b = pack_len[b] tokens) and key/value rows [cu_kv[b], cu_kv[b+1]) =
