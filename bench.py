@@ -21,6 +21,7 @@ from __future__ import annotations
 import argparse
 import dataclasses
 import json
+import math
 import os
 import statistics
 import sys
@@ -335,6 +336,63 @@ def cache_gather(dev, steps, warmup, layers=36):
                 kept=len(keep))
 
 
+def verify_round(dev, steps, warmup, layers=36):
+    """One verify round's device work at the headline shapes (Qwen3-8B, 36
+    layers, B=8 x (8192 + 128)): the ancestor words, the attention of every
+    layer reading its KV store in place, the greedy accept over 1024 x 151936
+    logits and the accepted-path KV append of all layers.  The model's own
+    projections and MLPs are not part of it.  Timed as eager launches and as
+    one replay of a HIP graph that captured the same round."""
+    import torch
+    from cast_amd import greedy_accept, scenarios, serving, tree_bitmask
+    from cast_amd.tree_attn import plan, store_tree_attention
+    wl = scenarios.qwen3_headline()
+    meta = wl.meta_tensors(dev)
+    B, Hkv, Hq, D, S = wl.B, wl.Hkv, wl.Hq, wl.D, int(wl.prefix_len[0])
+    cap = S + 320
+    g = torch.Generator(device=dev).manual_seed(11)
+    bf = torch.bfloat16
+    k_st = [torch.randn((B, Hkv, cap, D), generator=g, device=dev).to(bf) for _ in range(layers)]
+    v_st = [torch.randn((B, Hkv, cap, D), generator=g, device=dev).to(bf) for _ in range(layers)]
+    k_pk = [torch.randn((wl.total_q, Hkv, D), generator=g, device=dev).to(bf).transpose(0, 1) for _ in range(layers)]
+    v_pk = [torch.randn((wl.total_q, Hkv, D), generator=g, device=dev).to(bf).transpose(0, 1) for _ in range(layers)]
+    q = (torch.randn((wl.total_q, Hq, D), generator=g, device=dev) / math.sqrt(D)).to(bf)
+    outs = [torch.empty_like(q) for _ in range(layers)]
+    logits, _ = scenarios.planted_logits(wl, seed=0)
+    logits = logits.to(dev)
+    token = torch.from_numpy(wl.packed.token).to(dev)
+    store_len = torch.from_numpy(wl.prefix_len.astype("int32")).to(dev)
+    p = plan(B, wl.total_q, wl.total_kv, Hq, Hkv, D)
+    ws = torch.empty(max(p.workspace_bytes, 256), dtype=torch.uint8, device=dev)
+
+    def round_():
+        mask = tree_bitmask(meta["parent"], meta["cu_q"], 2)
+        for li in range(layers):
+            store_tree_attention(q, k_st[li], v_st[li], k_pk[li], v_pk[li], meta["cu_q"], meta["prefix_len"],
+                                 meta["pack_len"], mask, total_kv=wl.total_kv, out=outs[li], workspace=ws)
+        path, plen, _, _ = greedy_accept(logits, meta["cu_q"], meta["parent"], token)
+        # the append writes the accepted rows at fixed slots each round
+        serving.append_accepted(k_st, v_st, store_len, meta["cu_q"], path, plen, k_pk, v_pk)
+
+    eager = time_kernel(round_, steps, warmup)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        round_()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        round_()
+    replay = time_kernel(graph.replay, steps, warmup)
+    log(f"  verify round ({layers} layers, headline shapes): eager {eager / 1e3:.2f} ms, graph replay "
+        f"{replay / 1e3:.2f} ms")
+    res = dict(layers=layers, eager_ms=round(eager / 1e3, 3), graph_replay_ms=round(replay / 1e3, 3))
+    del k_st, v_st, k_pk, v_pk, graph
+    torch.cuda.empty_cache()
+    return res
+
+
 def graph_replay(dev, steps, warmup, layers=36):
     """The verify attention of one request (S=2048, P=16: launch-bound) over
     36 layers: 36 eager calls against one replay of a HIP graph that
@@ -477,6 +535,7 @@ def secondary(dev, steps, warmup):
     res["cache_gather"] = cache_gather(dev, steps, warmup)
     res["draft_trees"] = draft_trees(dev, steps, warmup)
     res["graph_replay"] = graph_replay(dev, steps, warmup)
+    res["verify_round"] = verify_round(dev, steps, warmup)
     res.update(bitmask_lines(dev, steps, warmup))
     return res
 
@@ -526,7 +585,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", choices=["kv_append", "cache_gather", "draft_trees", "store_layout", "tree_bitmask",
-                                       "graph_replay",
+                                       "graph_replay", "verify_round",
                                        *ATTN_WORKLOADS],
                     help="only run one secondary workload (for kernel profiles); prints its JSON")
     ap.add_argument("--clock-trace", type=int, default=0, metavar="N",
@@ -563,7 +622,8 @@ def main():
             print(json.dumps({args.only: attn_workload(dev, args.only, args.steps, args.warmup)}), flush=True)
             return
         fn = {"kv_append": kv_append, "cache_gather": cache_gather, "draft_trees": draft_trees,
-              "store_layout": store_layout, "tree_bitmask": bitmask_lines, "graph_replay": graph_replay}[args.only]
+              "store_layout": store_layout, "tree_bitmask": bitmask_lines, "graph_replay": graph_replay,
+              "verify_round": verify_round}[args.only]
         print(json.dumps({args.only: fn(dev, args.steps, args.warmup)}), flush=True)
         return
     log(f"device: {torch.cuda.get_device_name(dev)}")
