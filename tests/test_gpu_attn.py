@@ -124,6 +124,37 @@ def test_many_splits_both_combine_paths(gpu, kv_split):
                    label=f"headline-split{kv_split}")
 
 
+@pytest.mark.parametrize("make", [SC.qwen3_headline, SC.stress_mixed], ids=["headline", "stress-b32"])
+def test_full_size_exact_properties(gpu, make):
+    # size-independent checks at the benchmark shapes, bit for bit:
+    #  - V -> 2V (exact in bf16) doubles the output and keeps the LSE;
+    #  - permuting the KV heads, with their query-head groups, permutes the
+    #    output: each (request, head) sums the same keys in the same order,
+    #    whichever workgroup the schedule gives it
+    from cast_amd import varlen_tree_attention
+    wl = make()
+    print(f"case full-size-properties {wl.name}: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv}", flush=True)
+    q, k, v = wl.qkv(device=gpu)
+    meta = wl.meta_tensors(gpu)
+    mask = torch.from_numpy(_words(wl).view(np.int64).copy()).to(gpu)
+
+    def run(q_, k_, v_):
+        o, l = varlen_tree_attention(q_, k_, v_, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                                     mask, return_lse=True)
+        torch.cuda.synchronize()
+        return o, l
+
+    out, lse = run(q, k, v)
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    out2, lse2 = run(q, k, v * 2)
+    assert torch.equal(out2, out * 2) and torch.equal(lse2, lse)
+    G = wl.Hq // wl.Hkv
+    perm = torch.randperm(wl.Hkv, generator=torch.Generator().manual_seed(3)).to(gpu)
+    qperm = (perm[:, None] * G + torch.arange(G, device=gpu)[None, :]).reshape(-1)
+    out3, lse3 = run(q[:, qperm].contiguous(), k[:, perm].contiguous(), v[:, perm].contiguous())
+    assert torch.equal(out3, out[:, qperm]) and torch.equal(lse3, lse[:, qperm])
+
+
 def test_empty_rows_give_zero_and_minus_inf(gpu):
     from cast_amd import varlen_tree_attention
     wl = SC.random_parent_batch(seed=9, B=2, Hq=8, Hkv=2, D=128, s_lo=0, s_hi=1, p_lo=5, p_hi=6, dtype="bf16")
