@@ -79,6 +79,14 @@ def test_store_reference_scenario(gpu, dtype):
     _check_store(SC.random_parent_batch(seed=1, dtype=dtype), gpu, label=f"store-reference-scenario-{dtype}")
 
 
+@pytest.mark.parametrize("dtype,B,kv_split", [("bf16", 4, 0), ("fp32", 4, 128), ("bf16", 70, 0), ("fp32", 70, -1)])
+def test_store_head_dim_64_and_large_batches(gpu, dtype, B, kv_split):
+    # D = 64 instances and batches past 64 requests (batch-order schedule) in the store layout
+    wl = SC.random_parent_batch(seed=B + 3, B=B, Hq=16, Hkv=4, D=64, s_lo=30, s_hi=600, p_lo=1, p_hi=90,
+                                dtype=dtype, qkv_scale=0.5)
+    _check_store(wl, gpu, kv_split=kv_split, label=f"store-d64-b{B}-{dtype}-split{kv_split}")
+
+
 def test_store_empty_and_tiny_prefixes(gpu):
     # S_b in {0, 1, 2}: tiles that start inside the pack, single-key prefixes
     wl = SC.random_parent_batch(seed=2, s_lo=0, s_hi=3, p_lo=1, p_hi=80, dtype="bf16")
