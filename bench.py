@@ -540,6 +540,70 @@ def secondary(dev, steps, warmup):
     return res
 
 
+def mfma_ceiling(dev, steps, warmup, sets=3):
+    """What the matrix pipes sustain at the headline attention kernel's launch
+    shape (cast_mfma_ceiling): 256 workgroups x 8 waves x 65 tiles x 32
+    v_mfma_f32_32x32x16_bf16, the headline's exact MFMA count, with operands in
+    registers, then read from LDS, then with the per-tile barrier as well.  The
+    headline attention kernel is timed in the same process before and after,
+    so the ratio does not depend on the box's sustained clock."""
+    import torch
+    from cast_amd import _lib, scenarios
+    lib = _lib.load()
+    wl = scenarios.qwen3_headline()
+    h = Harness(wl, dev, sets=sets, kv_split=0)
+    grid, tiles = 256, 65
+    flop = grid * 8 * tiles * 32 * 32 * 32 * 16 * 2
+    g = torch.Generator(device=dev).manual_seed(5)
+    src = torch.randn(1 << 20, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty(grid * 512, dtype=torch.float32, device=dev)
+    clk = torch.zeros(2 * grid, dtype=torch.int64, device=dev)
+    stream = _lib.stream_of(src)
+
+    def attention():
+        t = h.time(steps, warmup)
+        return dict(us=round(t["attn_mean_us"], 2), tflops=round(wl.algorithmic_flops() / t["attn_mean_us"] / 1e6, 1))
+
+    def run(mode):
+        def launch():
+            _lib.check(lib.cast_mfma_ceiling(_lib.ptr(src), src.numel() // 8, _lib.ptr(out), _lib.ptr(clk), grid,
+                                             tiles, mode, stream), "cast_mfma_ceiling")
+        for _ in range(warmup):
+            launch()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+        torch.cuda.synchronize()
+        for e in ev:
+            e[0].record()
+            launch()
+            e[1].record()
+        torch.cuda.synchronize()
+        us = statistics.fmean(e[0].elapsed_time(e[1]) * 1e3 for e in ev)
+        cw = clk.view(grid, 2).cpu().tolist()
+        ghz = sorted(c / (w / 100.0) / 1e3 for c, w in cw if w > 0)
+        if not torch.isfinite(out).all():
+            raise RuntimeError("mfma ceiling: non-finite accumulators")
+        tf = flop / us / 1e6
+        return dict(us=round(us, 2), tflops=round(tf, 1), frac=round(tf / (PEAK_MFMA_BF16 / 1e12), 4),
+                    ghz_median=round(statistics.median(ghz), 3), ghz_min=round(ghz[0], 3), ghz_max=round(ghz[-1], 3))
+
+    before = attention()
+    log(f"  attention kernel {before['us']} us = {before['tflops']} TFLOP/s")
+    modes = {}
+    for name, mode in (("registers", 0), ("lds_operands", 1), ("lds_operands_barrier", 3)):
+        modes[name] = run(mode)
+        r = modes[name]
+        log(f"  mfma ceiling, {name}: {r['us']} us = {r['tflops']} TFLOP/s ({r['frac']} of peak) "
+            f"at {r['ghz_median']} GHz ({r['ghz_min']}-{r['ghz_max']})")
+    after = attention()
+    log(f"  attention kernel {after['us']} us = {after['tflops']} TFLOP/s")
+    best = max(before["tflops"], after["tflops"])
+    return dict(workload=wl.name, grid=grid, tiles=tiles, waves=8, flop_per_launch=flop,
+                algorithmic_flop=wl.algorithmic_flops(), steps=steps, warmup=warmup, modes=modes,
+                attention_before=before, attention_after=after,
+                attention_of_register_ceiling=round(best / modes["registers"]["tflops"], 3),
+                attention_of_lds_ceiling=round(best / modes["lds_operands_barrier"]["tflops"], 3))
+
+
 def clock_trace(dev, n, sets):
     """The headline call n times from a cold start, each followed by a shader
     clock sample (cast_clock_sample): per call the event time, the clock and
@@ -590,6 +654,9 @@ def main():
                     help="only run one secondary workload (for kernel profiles); prints its JSON")
     ap.add_argument("--clock-trace", type=int, default=0, metavar="N",
                     help="only run N headline calls from a cold start, each followed by a shader clock sample")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only time the MFMA ceiling loops at the headline kernel's launch shape, bracketed by "
+                         "the headline attention kernel")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches), to scale HBM byte counters")
     args = ap.parse_args()
@@ -613,6 +680,9 @@ def main():
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
+        return
+    if args.mfma_ceiling:
+        print(json.dumps({"mfma_ceiling": mfma_ceiling(dev, args.steps, args.warmup, args.sets)}), flush=True)
         return
     if args.clock_trace:
         print(json.dumps({"clock_trace": clock_trace(dev, args.clock_trace, args.sets)}), flush=True)

@@ -53,6 +53,7 @@ SIGNATURES = {
     "cast_draft_topk_workspace_size": ([_I32, _I32, _I32, _I32, _I32], _SZ),
     "cast_build_trees": ([_P, _P, _I32, _I32, _I32, _I32] + [_P] * 8, ctypes.c_int),
     "cast_clock_sample": ([_P, _I32, _I32, _P], ctypes.c_int),
+    "cast_mfma_ceiling": ([_P, _I64, _P, _P, _I32, _I32, _I32, _P], ctypes.c_int),
     "cast_greedy_accept": ([_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P], ctypes.c_int),
 }
 

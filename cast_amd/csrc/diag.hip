@@ -1,6 +1,8 @@
-// Measurement aid (no counterpart in the reference): samples the shader
-// clock next to the constant 100 MHz clock, so that a benchmark can tell a
-// change of clock frequency from a change of cycles per call.
+// Measurement aids (no counterpart in the reference): a shader clock sample
+// next to the constant 100 MHz clock, so that a benchmark can tell a change
+// of clock frequency from a change of cycles per call; and an MFMA ceiling
+// loop at the attention kernel's launch shape, which measures what the
+// matrix pipes sustain on this part under that load.
 #include "cast_common.hpp"
 
 namespace cast {
@@ -17,7 +19,96 @@ __global__ void clock_sample_kernel(uint64_t *out, int32_t slot, int32_t iters) 
     out[2 * slot + 1] = (w1 - w0) + (x == 12345.f ? 1u : 0u);   // keeps the chain live
 }
 
+// MFMA ceiling at the bf16 attention kernel's launch shape: 512-thread
+// workgroups, two waves per SIMD, and per wave `tiles` rounds of that
+// kernel's 32 v_mfma_f32_32x32x16_bf16 per 64-key tile (two 8-deep S^T
+// chains over the head dim, then 16 into four O^T blocks), with no softmax
+// and no global loads.  MODE bit 0 reads every A operand from LDS at the
+// kernel's K / V^T addresses (ds_read_b128, double-buffered tiles); bit 1
+// adds the per-tile workgroup barrier.  B operands stay in registers, as the
+// kernel's Q^T does.  The S^T chains run on across tiles (no reset) so that
+// every product stays live without VALU work; the accumulators are summed
+// into out[] at the end.  Wave 0 of each workgroup records its shader
+// cycles and 100 MHz ticks in clk[2 * block], clk[2 * block + 1].
+constexpr int kCeilNT = 512;
+
+template <int MODE>
+__global__ __launch_bounds__(kCeilNT) __attribute__((amdgpu_waves_per_eu(2)))
+void mfma_ceiling_kernel(const bf16x8 *__restrict__ src, uint32_t src_chunks, float *__restrict__ out,
+                         uint64_t *__restrict__ clk, int32_t tiles) {
+    constexpr int KPAD = 136, VPAD = 72;              // the attention kernel's LDS row strides (D = 128)
+    constexpr int TILE = 64 * KPAD + 128 * VPAD;      // K [64][KPAD] then V^T [128][VPAD], elements
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * TILE];
+    const uint64_t c0 = clock64(), w0 = wall_clock64();
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+    bf16x8 a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = src[(uint32_t)(tid * 16 + i) % src_chunks];
+        b[i] = src[(uint32_t)(tid * 16 + 8 + i) % src_chunks];
+    }
+    if constexpr (MODE & 1) {
+        for (int c = tid; c < 2 * TILE / 8; c += kCeilNT)
+            *reinterpret_cast<bf16x8 *>(&lds[c * 8]) = src[(uint32_t)c % src_chunks];
+        __syncthreads();
+    }
+    floatx16 s[2], o[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) s[i] = floatx16{};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = floatx16{};
+    for (int t = 0; t < tiles; ++t) {
+        if constexpr ((MODE & 2) != 0) __syncthreads();
+        else __asm__ volatile("" ::: "memory");       // keeps the LDS reads inside the loop
+        const uint16_t *K = &lds[(t & 1) * TILE];
+        const uint16_t *V = K + 64 * KPAD;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int ds = 0; ds < 8; ++ds) {
+                bf16x8 x = a[ds];
+                if constexpr (MODE & 1) x = *reinterpret_cast<const bf16x8 *>(&K[(kb * 32 + l32) * KPAD + ds * 16 + g * 8]);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, b[ds], s[kb], 0, 0, 0);
+            }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    bf16x8 x = a[(kb * 2 + hf + db) & 7];
+                    if constexpr (MODE & 1)
+                        x = *reinterpret_cast<const bf16x8 *>(&V[(db * 32 + l32) * VPAD + kb * 32 + hf * 16 + g * 8]);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, b[kb * 2 + hf], o[db], 0, 0, 0);
+                }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc += s[0][e] + s[1][e] + o[0][e] + o[1][e] + o[2][e] + o[3][e];
+    out[(int64_t)blockIdx.x * kCeilNT + tid] = acc;
+    if (tid == 0) {
+        clk[2 * blockIdx.x] = clock64() - c0;
+        clk[2 * blockIdx.x + 1] = wall_clock64() - w0;
+    }
+}
+
 }  // namespace cast
+
+extern "C" int cast_mfma_ceiling(const void *src, int64_t src_chunks, float *out, uint64_t *clk, int32_t grid,
+                                 int32_t tiles, int32_t mode, cast_stream_t stream) {
+    if (!src || !out || !clk) return CAST_ERR_NULL_POINTER;
+    if (src_chunks < 1 || src_chunks > INT32_MAX || grid < 1 || grid > (1 << 20) || tiles < 0) return CAST_ERR_SHAPE;
+    const auto *s8 = static_cast<const cast::bf16x8 *>(src);
+    const uint32_t n = (uint32_t)src_chunks;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (mode) {
+    case 0: cast::mfma_ceiling_kernel<0><<<grid, cast::kCeilNT, 0, st>>>(s8, n, out, clk, tiles); break;
+    case 1: cast::mfma_ceiling_kernel<1><<<grid, cast::kCeilNT, 0, st>>>(s8, n, out, clk, tiles); break;
+    case 3: cast::mfma_ceiling_kernel<3><<<grid, cast::kCeilNT, 0, st>>>(s8, n, out, clk, tiles); break;
+    default: return CAST_ERR_SHAPE;
+    }
+    return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
+}
 
 extern "C" int cast_clock_sample(uint64_t *out, int32_t slot, int32_t iters, cast_stream_t stream) {
     if (!out) return CAST_ERR_NULL_POINTER;

@@ -246,3 +246,15 @@ def test_build_trees_refuses_host_budgets_above_127():
     for bad in (128, -1, [10, 200]):
         with pytest.raises(ValueError, match="budget must be in"):
             build_trees(ti, tl, bad)
+
+
+def test_mfma_ceiling_host_validation(lib):
+    # the measurement aid rejects bad arguments before any launch
+    fake = 1 << 20
+    assert lib.cast_mfma_ceiling(None, 8, fake, fake, 1, 1, 0, None) == 1
+    assert lib.cast_mfma_ceiling(fake, 0, fake, fake, 1, 1, 0, None) == 7
+    assert lib.cast_mfma_ceiling(fake, 1 << 31, fake, fake, 1, 1, 0, None) == 7
+    assert lib.cast_mfma_ceiling(fake, 8, fake, fake, 0, 1, 0, None) == 7
+    assert lib.cast_mfma_ceiling(fake, 8, fake, fake, 1, -1, 0, None) == 7
+    for mode in (2, 4, -1):
+        assert lib.cast_mfma_ceiling(fake, 8, fake, fake, 1, 1, mode, None) == 7
