@@ -38,12 +38,16 @@ __all__ = ["__version__", "MAX_PACK", "PackedTrees", "TreeNode", "ancestor_matri
 
 
 def __getattr__(name):
-    module = _LAZY.get(name)
-    if module is None:
+    """Device-side names: import their module on first use and keep the
+    result in this module's namespace, so the hook runs once per name."""
+    home = _LAZY.get(name)
+    if home is None:
         raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
-    from importlib import import_module
-    return getattr(import_module(f".{module}", __name__), name)
+    import importlib
+    value = getattr(importlib.import_module(f"{__name__}.{home}"), name)
+    globals()[name] = value
+    return value
 
 
 def __dir__():
-    return sorted(__all__)
+    return list(__all__)    # dir() sorts
