@@ -322,11 +322,14 @@ def cache_gather(dev, steps, warmup, layers=36):
         gather_cache(cache, n_prefix, keep)
 
     def reference_flow():
+        # what cast_trees/verify.py:48-60 does: one position index, then every
+        # layer's K and V gathered whole along the sequence axis
         restore()
-        sel = torch.cat([torch.arange(n_prefix, device=dev), torch.tensor([n_prefix + i for i in keep], device=dev)])
-        for i in range(n_layers):
-            k, v = get(i)
-            put(i, k.index_select(2, sel), v.index_select(2, sel))
+        positions = torch.cat([torch.arange(n_prefix, device=dev),
+                               torch.tensor([n_prefix + j for j in keep], device=dev)])
+        for layer in range(n_layers):
+            k_old, v_old = get(layer)
+            put(layer, torch.index_select(k_old, 2, positions), torch.index_select(v_old, 2, positions))
 
     t_d = time_kernel(device, steps, warmup)
     t_r = time_kernel(reference_flow, steps, warmup)

@@ -68,11 +68,14 @@ def test_tree_is_prefix_closed():
     idx, lp = T.block_topk(np.random.default_rng(3).normal(size=(15, 100)) * 3, 8)
     nodes = T.build_tree(idx, lp, 127)
     assert len(nodes) == 127
-    for i, nd in enumerate(nodes):
-        assert nd.parent < i
-        if nd.parent >= 0:
-            assert nodes[nd.parent].depth == nd.depth - 1
-            assert nodes[nd.parent].score >= nd.score
+    par = np.array([n.parent for n in nodes])
+    depth = np.array([n.depth for n in nodes])
+    score = np.array([n.score for n in nodes])
+    assert (par < np.arange(len(nodes))).all()                 # every parent listed first
+    top, kid = par < 0, np.nonzero(par >= 0)[0]
+    assert (depth[top] == 1).all()
+    assert (depth[kid] == depth[par[kid]] + 1).all()           # one level below its parent
+    assert (score[kid] <= score[par[kid]]).all()               # log-probs never add score
 
 
 def test_select_global_topk_matches_reference():
@@ -83,21 +86,25 @@ def test_select_global_topk_matches_reference():
     split = T.select_global_topk(forest, 64)
     want = FIX["global_topk"]["split"]
     assert [_triples(t) for t in split] == [[w[:3] for w in t] for t in want]
-    assert sum(len(t) for t in split) == 64
+    assert sum(map(len, split)) == 64
 
 
 def test_ancestor_matrix_is_the_chain_walk():
-    # tests/test_tree.py:58-67
+    # the property of tests/test_tree.py:58-67, checked by walking every
+    # packed row's parent chain at once (one step up per pass), independent
+    # of the row-inheriting recurrence the product uses
     idx, lp = T.block_topk(np.random.default_rng(0).normal(size=(15, 100)) * 3, 8)
     nodes = T.build_tree(idx, lp, budget=31)
     vis = T.ancestor_matrix(nodes)
-    assert vis[0].nonzero()[0].tolist() == [0]
-    for i, nd in enumerate(nodes):
-        chain, j = {0, i + 1}, nd.parent
-        while j >= 0:
-            chain.add(j + 1)
-            j = nodes[j].parent
-        assert set(vis[i + 1].nonzero()[0].tolist()) == chain
+    up = np.array([-1] + [n.parent + 1 for n in nodes])        # packed parent, -1 above the root
+    want = np.eye(len(up), dtype=bool)
+    at = np.arange(len(up))
+    while (at >= 0).any():
+        at = np.where(at >= 0, up[np.maximum(at, 0)], -1)
+        rows = np.nonzero(at >= 0)[0]
+        want[rows, at[rows]] = True
+    assert want[1:, 0].all() and not want[0, 1:].any()          # the root is everyone's ancestor, alone on row 0
+    assert np.array_equal(vis, want)
 
 
 def test_pack_trees_layout_and_errors():
