@@ -99,8 +99,10 @@ def test_edge_packs(gpu):
 
 
 def test_gqa_ratios_and_head_dim_64(gpu):
+    # includes one KV head for all query heads (MQA): a pack of 128 tokens is
+    # then 4096 query rows, 16 row blocks of one (request, KV head)
     for Hq, Hkv, D, dt in [(8, 8, 64, "bf16"), (16, 2, 64, "bf16"), (64, 8, 128, "bf16"), (12, 4, 96, "bf16"),
-                           (8, 2, 128, "fp32")]:
+                           (8, 2, 128, "fp32"), (32, 1, 128, "bf16"), (16, 1, 64, "fp32")]:
         wl = SC.random_parent_batch(seed=Hq + D, B=3, Hq=Hq, Hkv=Hkv, D=D, s_lo=50, s_hi=700, p_lo=1, p_hi=129,
                                     dtype=dt, qkv_scale=0.5)
         _run_and_check(wl, gpu, label=f"gqa{Hq}/{Hkv}-D{D}-{dt}")
