@@ -567,7 +567,7 @@ def mfma_ceiling(dev, steps, warmup, sets=3):
         t = h.time(steps, warmup)
         return dict(us=round(t["attn_mean_us"], 2), tflops=round(wl.algorithmic_flops() / t["attn_mean_us"] / 1e6, 1))
 
-    def run(mode):
+    def run(mode, grid=grid):
         def launch():
             _lib.check(lib.cast_mfma_ceiling(_lib.ptr(src), src.numel() // 8, _lib.ptr(out), _lib.ptr(clk), grid,
                                              tiles, mode, stream), "cast_mfma_ceiling")
@@ -581,11 +581,11 @@ def mfma_ceiling(dev, steps, warmup, sets=3):
             e[1].record()
         torch.cuda.synchronize()
         us = statistics.fmean(e[0].elapsed_time(e[1]) * 1e3 for e in ev)
-        cw = clk.view(grid, 2).cpu().tolist()
+        cw = clk[:2 * grid].view(grid, 2).cpu().tolist()
         ghz = sorted(c / (w / 100.0) / 1e3 for c, w in cw if w > 0)
         if not torch.isfinite(out).all():
             raise RuntimeError("mfma ceiling: non-finite accumulators")
-        tf = flop / us / 1e6
+        tf = flop * grid / 256 / us / 1e6
         return dict(us=round(us, 2), tflops=round(tf, 1), frac=round(tf / (PEAK_MFMA_BF16 / 1e12), 4),
                     ghz_median=round(statistics.median(ghz), 3), ghz_min=round(ghz[0], 3), ghz_max=round(ghz[-1], 3))
 
@@ -597,11 +597,19 @@ def mfma_ceiling(dev, steps, warmup, sets=3):
         r = modes[name]
         log(f"  mfma ceiling, {name}: {r['us']} us = {r['tflops']} TFLOP/s ({r['frac']} of peak) "
             f"at {r['ghz_median']} GHz ({r['ghz_min']}-{r['ghz_max']})")
+    # the register loop on fewer CUs (one workgroup per CU): a clock that rises
+    # as CUs go idle is set by the power limit, not by a fixed MFMA clock
+    fewer = {}
+    for g in (128, 64, 32):
+        r = run(0, g)
+        fewer[str(g)] = dict(us=r["us"], ghz_median=r["ghz_median"])
+        log(f"  mfma ceiling, registers, {g} workgroups: {r['us']} us at {r['ghz_median']} GHz")
     after = attention()
     log(f"  attention kernel {after['us']} us = {after['tflops']} TFLOP/s")
     best = max(before["tflops"], after["tflops"])
     return dict(workload=wl.name, grid=grid, tiles=tiles, waves=8, flop_per_launch=flop,
                 algorithmic_flop=wl.algorithmic_flops(), steps=steps, warmup=warmup, modes=modes,
+                registers_on_fewer_workgroups=fewer,
                 attention_before=before, attention_after=after,
                 attention_of_register_ceiling=round(best / modes["registers"]["tflops"], 3),
                 attention_of_lds_ceiling=round(best / modes["lds_operands_barrier"]["tflops"], 3))
