@@ -12,9 +12,12 @@ is bracketed by HIP events on the launch stream: attention kernel, split-K
 combine.  One JSON line goes to stdout; progress goes to stderr.
 
 Also reported: the roofline of the attention kernel (binding side from the
-algorithmic bytes and flops), the HBM fraction the metric names, the CPU
-oracle timed on host cores on a one-request sample, and secondary workloads
-(bitmask and greedy-accept kernels, the other benchmark shapes).
+algorithmic bytes and flops), the HBM fraction the metric names, the MFMA
+ceiling of the kernel's launch shape timed right after the headline calls
+(what the part sustains in that clock state, and the kernel's fraction of
+it), the CPU oracle timed on host cores on a one-request sample, and
+secondary workloads (bitmask and greedy-accept kernels, the other benchmark
+shapes).
 """
 from __future__ import annotations
 
@@ -543,34 +546,30 @@ def secondary(dev, steps, warmup):
     return res
 
 
-def mfma_ceiling(dev, steps, warmup, sets=3):
-    """What the matrix pipes sustain at the headline attention kernel's launch
-    shape (cast_mfma_ceiling): 256 workgroups x 8 waves x 65 tiles x 32
-    v_mfma_f32_32x32x16_bf16, the headline's exact MFMA count, with operands in
-    registers, then read from LDS, then with the per-tile barrier as well.  The
-    headline attention kernel is timed in the same process before and after,
-    so the ratio does not depend on the box's sustained clock."""
-    import torch
-    from cast_amd import _lib, scenarios
-    lib = _lib.load()
-    wl = scenarios.qwen3_headline()
-    h = Harness(wl, dev, sets=sets, kv_split=0)
-    grid, tiles = 256, 65
-    flop = grid * 8 * tiles * 32 * 32 * 32 * 16 * 2
-    g = torch.Generator(device=dev).manual_seed(5)
-    src = torch.randn(1 << 20, generator=g, device=dev).to(torch.bfloat16)
-    out = torch.empty(grid * 512, dtype=torch.float32, device=dev)
-    clk = torch.zeros(2 * grid, dtype=torch.int64, device=dev)
-    stream = _lib.stream_of(src)
+class CeilingLoop:
+    """cast_mfma_ceiling at the headline attention kernel's launch shape:
+    `grid` workgroups x 8 waves x 65 tiles x 32 v_mfma_f32_32x32x16_bf16
+    (at grid 256, the headline's exact MFMA count)."""
+    TILES = 65
 
-    def attention():
-        t = h.time(steps, warmup)
-        return dict(us=round(t["attn_mean_us"], 2), tflops=round(wl.algorithmic_flops() / t["attn_mean_us"] / 1e6, 1))
+    def __init__(self, dev):
+        import torch
+        from cast_amd import _lib
+        self.lib, self._lib = _lib.load(), _lib
+        g = torch.Generator(device=dev).manual_seed(5)
+        self.src = torch.randn(1 << 20, generator=g, device=dev).to(torch.bfloat16)
+        self.out = torch.empty(256 * 512, dtype=torch.float32, device=dev)
+        self.clk = torch.zeros(2 * 256, dtype=torch.int64, device=dev)
+        self.stream = _lib.stream_of(self.src)
 
-    def run(mode, grid=grid):
+    def run(self, mode, steps, warmup, grid=256):
+        import torch
+        L = self._lib
+
         def launch():
-            _lib.check(lib.cast_mfma_ceiling(_lib.ptr(src), src.numel() // 8, _lib.ptr(out), _lib.ptr(clk), grid,
-                                             tiles, mode, stream), "cast_mfma_ceiling")
+            L.check(self.lib.cast_mfma_ceiling(L.ptr(self.src), self.src.numel() // 8, L.ptr(self.out),
+                                               L.ptr(self.clk), grid, self.TILES, mode, self.stream),
+                    "cast_mfma_ceiling")
         for _ in range(warmup):
             launch()
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
@@ -581,33 +580,51 @@ def mfma_ceiling(dev, steps, warmup, sets=3):
             e[1].record()
         torch.cuda.synchronize()
         us = statistics.fmean(e[0].elapsed_time(e[1]) * 1e3 for e in ev)
-        cw = clk[:2 * grid].view(grid, 2).cpu().tolist()
+        cw = self.clk[:2 * grid].view(grid, 2).cpu().tolist()
         ghz = sorted(c / (w / 100.0) / 1e3 for c, w in cw if w > 0)
-        if not torch.isfinite(out).all():
+        if not torch.isfinite(self.out[:grid * 512]).all():
             raise RuntimeError("mfma ceiling: non-finite accumulators")
-        tf = flop * grid / 256 / us / 1e6
+        flop = grid * 8 * self.TILES * 32 * 32 * 32 * 16 * 2
+        tf = flop / us / 1e6
         return dict(us=round(us, 2), tflops=round(tf, 1), frac=round(tf / (PEAK_MFMA_BF16 / 1e12), 4),
                     ghz_median=round(statistics.median(ghz), 3), ghz_min=round(ghz[0], 3), ghz_max=round(ghz[-1], 3))
+
+
+def mfma_ceiling(dev, steps, warmup, sets=3):
+    """What the matrix pipes sustain at the headline attention kernel's launch
+    shape (cast_mfma_ceiling): 256 workgroups x 8 waves x 65 tiles x 32
+    v_mfma_f32_32x32x16_bf16, the headline's exact MFMA count, with operands in
+    registers, then read from LDS, then with the per-tile barrier as well.  The
+    headline attention kernel is timed in the same process before and after,
+    so the ratio does not depend on the box's sustained clock."""
+    from cast_amd import scenarios
+    wl = scenarios.qwen3_headline()
+    h = Harness(wl, dev, sets=sets, kv_split=0)
+    loop = CeilingLoop(dev)
+    flop = 256 * 8 * loop.TILES * 32 * 32 * 32 * 16 * 2
+
+    def attention():
+        t = h.time(steps, warmup)
+        return dict(us=round(t["attn_mean_us"], 2), tflops=round(wl.algorithmic_flops() / t["attn_mean_us"] / 1e6, 1))
 
     before = attention()
     log(f"  attention kernel {before['us']} us = {before['tflops']} TFLOP/s")
     modes = {}
     for name, mode in (("registers", 0), ("lds_operands", 1), ("lds_operands_barrier", 3)):
-        modes[name] = run(mode)
-        r = modes[name]
+        modes[name] = r = loop.run(mode, steps, warmup)
         log(f"  mfma ceiling, {name}: {r['us']} us = {r['tflops']} TFLOP/s ({r['frac']} of peak) "
             f"at {r['ghz_median']} GHz ({r['ghz_min']}-{r['ghz_max']})")
     # the register loop on fewer CUs (one workgroup per CU): a clock that rises
     # as CUs go idle is set by the power limit, not by a fixed MFMA clock
     fewer = {}
     for g in (128, 64, 32):
-        r = run(0, g)
+        r = loop.run(0, steps, warmup, grid=g)
         fewer[str(g)] = dict(us=r["us"], ghz_median=r["ghz_median"])
         log(f"  mfma ceiling, registers, {g} workgroups: {r['us']} us at {r['ghz_median']} GHz")
     after = attention()
     log(f"  attention kernel {after['us']} us = {after['tflops']} TFLOP/s")
     best = max(before["tflops"], after["tflops"])
-    return dict(workload=wl.name, grid=grid, tiles=tiles, waves=8, flop_per_launch=flop,
+    return dict(workload=wl.name, grid=256, tiles=loop.TILES, waves=8, flop_per_launch=flop,
                 algorithmic_flop=wl.algorithmic_flops(), steps=steps, warmup=warmup, modes=modes,
                 registers_on_fewer_workgroups=fewer,
                 attention_before=before, attention_after=after,
@@ -746,6 +763,15 @@ def main():
         "call_mean_us": round(t["call_mean_us"], 2), "host_wall_us": round(t["wall_us"], 2),
         "algorithmic_bytes": wl.algorithmic_bytes(), "algorithmic_flops": wl.algorithmic_flops(),
     }
+    # the practical MFMA ceiling of this launch shape, timed right after the
+    # headline calls (same clock state): the headline's MFMA count with LDS
+    # operand reads and the per-tile barrier, no softmax and no loads
+    ceil = CeilingLoop(dev).run(3, args.steps, min(args.warmup, 5))
+    ceil["attention_frac_of_ceiling"] = round(rl["achieved"] / ceil["tflops"], 4)
+    ceil["loop"] = "lds_operands_barrier"
+    line["mfma_ceiling"] = ceil
+    log(f"  mfma ceiling (LDS operands + barrier): {ceil['tflops']} TFLOP/s ({ceil['frac']} of peak) at "
+        f"{ceil['ghz_median']} GHz; attention kernel at {ceil['attention_frac_of_ceiling']} of it")
     del h
     torch.cuda.empty_cache()
     if not args.no_secondary:
