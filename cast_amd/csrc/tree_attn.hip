@@ -1230,8 +1230,10 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
 }
 
 // --------------------------------------------------------------------------
-// Generic kernel: fp32 or bf16 inputs, any head_dim <= 128 (multiple of 8),
+// Generic kernel: fp32 or bf16 inputs, any head_dim <= 256 (multiple of 8),
 // scalar FMA.  One workgroup = 16 query rows of one (request, KV head).
+// DMAX sizes the LDS tiles: 128 (42 KB) for head_dim <= 128, 256 (83 KB)
+// above, as the reference kernel takes any power-of-two head_dim.
 // --------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ float load_elem(const T *p);
@@ -1240,9 +1242,9 @@ __device__ __forceinline__ float load_elem<float>(const float *p) { return *p; }
 template <>
 __device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *p) { return bf16_to_float(*p); }
 
-template <typename T>
+template <typename T, int DMAX>
 __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int D) {
-    constexpr int R = 16, BK = 32, DMAX = 128;
+    constexpr int R = 16, BK = 32;
     __shared__ float Qs[R][DMAX];
     __shared__ float Ks[BK][DMAX + 1];
     __shared__ float Vs[BK][DMAX];
@@ -1419,7 +1421,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         !mask || (!kv.store && !cu_kv))
         return CAST_ERR_NULL_POINTER;
     const bool mfma = mfma_path(dtype, head_dim);
-    if (!mfma && (head_dim > 128 || head_dim % 8)) return CAST_ERR_HEAD_DIM;
+    if (!mfma && (head_dim > 256 || head_dim % 8)) return CAST_ERR_HEAD_DIM;
     const int64_t esz = dtype == CAST_BF16 ? 2 : 4;
     int32_t max_rows = INT32_MAX;
     auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -1476,10 +1478,15 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         a.rows_wg = 16;
         const int64_t items = (int64_t)num_kv_heads * (((int64_t)total_q * a.G + 15) / 16 + batch);
         if (!(stages & kStageAttn)) return CAST_OK;
-        if (dtype == CAST_FP32)
-            tree_attn_generic_kernel<float><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
+        const bool wide = head_dim > 128;
+        if (dtype == CAST_FP32 && wide)
+            tree_attn_generic_kernel<float, 256><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
+        else if (dtype == CAST_FP32)
+            tree_attn_generic_kernel<float, 128><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
+        else if (wide)
+            tree_attn_generic_kernel<uint16_t, 256><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
         else
-            tree_attn_generic_kernel<uint16_t><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
+            tree_attn_generic_kernel<uint16_t, 128><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
         return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
     }
 

@@ -258,3 +258,12 @@ def test_mfma_ceiling_host_validation(lib):
     assert lib.cast_mfma_ceiling(fake, 8, fake, fake, 1, -1, 0, None) == 7
     for mode in (2, 4, -1):
         assert lib.cast_mfma_ceiling(fake, 8, fake, fake, 1, 1, mode, None) == 7
+
+
+def test_head_dim_bounds(lib):
+    # MFMA kernels take 64 and 128; the scalar kernel any other multiple of 8
+    # up to 256.  Out-of-range head dims are refused before any launch.
+    fake = 1 << 20
+    ptrs = dict(q=fake, k=fake, v=fake, out=fake, cu_q=fake, cu_kv=fake, prefix=fake, pack=fake, mask=fake)
+    for D in (264, 100, 4, 512):
+        assert _attn(lib, D=D, **ptrs) == 5, D

@@ -108,6 +108,15 @@ def test_gqa_ratios_and_head_dim_64(gpu):
         _run_and_check(wl, gpu, label=f"gqa{Hq}/{Hkv}-D{D}-{dt}")
 
 
+def test_head_dims_above_128(gpu):
+    # the reference kernel takes any power-of-two head_dim (tl.arange(0, D),
+    # tree_attn.py:36); here 192 and 256 run on the scalar kernel's wide tiles
+    for Hq, Hkv, D, dt in [(8, 2, 256, "bf16"), (4, 4, 256, "fp32"), (8, 4, 192, "bf16"), (4, 1, 136, "fp32")]:
+        wl = SC.random_parent_batch(seed=D + Hq, B=3, Hq=Hq, Hkv=Hkv, D=D, s_lo=20, s_hi=300, p_lo=1, p_hi=129,
+                                    dtype=dt, qkv_scale=0.5)
+        _run_and_check(wl, gpu, label=f"head-dim-{D}-{Hq}/{Hkv}-{dt}")
+
+
 @pytest.mark.parametrize("B,dtype,kv_split", [(64, "bf16", 0), (65, "bf16", 0), (65, "bf16", 192),
                                                (130, "bf16", 0), (130, "fp32", 256)])
 def test_batches_across_the_64_request_boundary(gpu, B, dtype, kv_split):
