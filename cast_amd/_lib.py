@@ -24,7 +24,7 @@ FLAG_BAD_OFFSETS = 2
 FLAG_BAD_PARENT = 4
 FLAG_TOO_LONG = 8
 
-BF16, FP32, FP64 = 0, 1, 2
+BF16, FP32, FP64, FP16 = 0, 1, 2, 3
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

@@ -8,9 +8,9 @@
 // Two kernels on the caller's stream:
 //   row_argmax   one workgroup per packed row: first index of the row
 //                maximum, NaN counting as the maximum (torch.argmax rule).
-//                Streams the logits once with 16-byte loads.  bf16 rows
-//                compare 16-bit order keys two at a time (see below), a row
-//                holding a NaN takes the exact element-by-element scan.
+//                Streams the logits once with 16-byte loads.  bf16 and fp16
+//                rows compare 16-bit order keys two at a time (see below), a
+//                row holding a NaN takes the exact element-by-element scan.
 //   tree_walk    one wave per request: starting at the root row, finds the
 //                first child (lowest pack index, i.e. node order) whose draft
 //                token equals the row's argmax with one ballot per level,
@@ -30,12 +30,18 @@ __device__ __forceinline__ bool better(float v1, int i1, float v2, int i2) {
     return v1 > v2 || (v1 == v2 && i1 < i2);
 }
 
+// Element formats of a logits row: F32 (float), or Bf16 / Fp16 (16-bit).
+struct F32 {};
+template <typename F>
+constexpr bool kHalf = !__is_same(F, F32);
+
 // The first index of the maximum of one row (base, vocab elements), NaN
 // counting as the maximum, element by element; the workgroup's 256 threads
 // call it together and thread 0 writes *out.
-template <bool BF16>
+template <typename F>
 __device__ void argmax_exact(const char *__restrict__ base, int32_t vocab, int32_t *__restrict__ out) {
     constexpr int NT = 256;
+    constexpr bool BF16 = kHalf<F>;     // 16-bit elements (bf16 or fp16)
     constexpr int EPC = BF16 ? 8 : 4;   // elements per 16-byte chunk
     const int tid = threadIdx.x;
     float best = -INFINITY;
@@ -59,7 +65,7 @@ __device__ void argmax_exact(const char *__restrict__ base, int32_t vocab, int32
             // vector element expression reads the vector's first element
             const uint32_t bits = w[BF16 ? (e >> 1) : e];
             if constexpr (BF16)
-                v = bf16_to_float((uint16_t)(bits >> ((e & 1) * 16)));
+                v = F::widen((uint16_t)(bits >> ((e & 1) * 16)));
             else
                 v = __builtin_bit_cast(float, bits);
             if (first && e == 0) {   // the thread's first element seeds the running best
@@ -89,7 +95,7 @@ __device__ void argmax_exact(const char *__restrict__ base, int32_t vocab, int32
     for (int i = nch * EPC + tid; i < vocab; i += NT) {
         float v;
         if constexpr (BF16)
-            v = bf16_to_float(reinterpret_cast<const uint16_t *>(base)[i]);
+            v = F::widen(reinterpret_cast<const uint16_t *>(base)[i]);
         else
             v = reinterpret_cast<const float *>(base)[i];
         if (bi == INT_MAX) {     // no vector chunk seeded this thread
@@ -125,19 +131,21 @@ __device__ void argmax_exact(const char *__restrict__ base, int32_t vocab, int32
     }
 }
 
-template <bool BF16>
+template <typename F>
 __global__ __launch_bounds__(256) void row_argmax_kernel(const void *__restrict__ logits, int64_t ld,
                                                          int32_t vocab, int32_t *__restrict__ argmax) {
-    const char *base = static_cast<const char *>(logits) + (size_t)blockIdx.x * (size_t)ld * (BF16 ? 2 : 4);
-    argmax_exact<BF16>(base, vocab, argmax + blockIdx.x);
+    const char *base = static_cast<const char *>(logits) + (size_t)blockIdx.x * (size_t)ld * (kHalf<F> ? 2 : 4);
+    argmax_exact<F>(base, vocab, argmax + blockIdx.x);
 }
 
-// ---- bf16 rows by order keys.  A bf16 value with magnitude bits m (sign
-// cleared) gets the 16-bit two's-complement key m when non-negative and -m
-// when negative.  Keys order exactly as the values do for every non-NaN
-// pair, and -0 and +0 share key 0, so equal values tie as the float compare
-// has them.  A NaN has m > 0x7f80 (the magnitude of infinity); a row that
-// holds one is left to the exact scan, since NaN outranks every value there.
+// ---- 16-bit rows by order keys.  A bf16 or fp16 value with magnitude bits
+// m (sign cleared) gets the 16-bit two's-complement key m when non-negative
+// and -m when negative: both are sign-magnitude formats whose magnitude bits
+// order as the magnitudes do.  Keys order exactly as the values do for every
+// non-NaN pair, and -0 and +0 share key 0, so equal values tie as the float
+// compare has them.  A NaN has m above the magnitude of infinity (0x7f80 in
+// bf16, 0x7c00 in fp16); a row that holds one is left to the exact scan,
+// since NaN outranks every value there.
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
@@ -160,9 +168,11 @@ __device__ __forceinline__ int bf16_key(uint16_t bits) {
 // order) and the first chunk holding it; then that chunk alone is read
 // again for the first element with the key.  Per element the scan costs
 // about three VALU operations against about nine for the float compare.
+template <typename F>   // Bf16 or Fp16
 __global__ __launch_bounds__(256) void row_argmax_bf16_kernel(const void *__restrict__ logits, int64_t ld,
                                                               int32_t vocab, int32_t *__restrict__ argmax) {
     constexpr int NT = 256;
+    constexpr unsigned short kInfMag = __is_same(F, Fp16) ? 0x7c00 : 0x7f80;
     constexpr int EPC = 8;
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
@@ -222,9 +232,9 @@ __global__ __launch_bounds__(256) void row_argmax_bf16_kernel(const void *__rest
             bi = i;
         }
     }
-    const bool nan = max(magmax[0], magmax[1]) > 0x7f80;
+    const bool nan = max(magmax[0], magmax[1]) > kInfMag;
     if (__syncthreads_or(nan)) {
-        argmax_exact<true>(base, vocab, argmax + row);
+        argmax_exact<F>(base, vocab, argmax + row);
         return;
     }
     // (key desc, index asc) over the workgroup
@@ -331,16 +341,18 @@ extern "C" int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t
                                   int32_t batch, int32_t total_q, int32_t *argmax, int32_t *path,
                                   int32_t *path_len, int64_t *bonus, int32_t *status, cast_stream_t stream) {
     if (batch < 0 || total_q < 0 || vocab <= 0 || logits_ld < vocab) return CAST_ERR_SHAPE;
-    if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
+    if (dtype != CAST_BF16 && dtype != CAST_FP16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
     if (batch == 0) return CAST_OK;
     if (!logits || !cu_q || !parent || !token || !argmax || !path || !path_len || !bonus)
         return CAST_ERR_NULL_POINTER;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (total_q > 0) {
         if (dtype == CAST_BF16)
-            row_argmax_bf16_kernel<<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
+            row_argmax_bf16_kernel<Bf16><<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
+        else if (dtype == CAST_FP16)
+            row_argmax_bf16_kernel<Fp16><<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
         else
-            row_argmax_kernel<false><<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
+            row_argmax_kernel<F32><<<total_q, 256, 0, s>>>(logits, logits_ld, vocab, argmax);
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     }
     tree_walk_kernel<<<batch, 64, 0, s>>>(cu_q, parent, token, argmax, total_q, path, path_len, bonus, status);

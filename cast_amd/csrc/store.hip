@@ -118,11 +118,11 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     if (layers < 0 || batch < 0 || total_q < 0 || cap < 0 || num_kv_heads <= 0 || head_dim <= 0 ||
         path_stride < kMaxPack)
         return CAST_ERR_SHAPE;
-    if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
+    if (dtype != CAST_BF16 && dtype != CAST_FP16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
     if (layers == 0 || batch == 0) return CAST_OK;
     if (!k_pack || !v_pack || !k_store || !v_store || !src_row || !path || !path_len || !store_len)
         return CAST_ERR_NULL_POINTER;
-    const int64_t esz = dtype == CAST_BF16 ? 2 : 4;
+    const int64_t esz = dtype == CAST_FP32 ? 4 : 2;   // a row copy: only the element size matters
     if ((head_dim * esz) % 16 || head_dim * esz > 16 * kAppendMaxChunks) return CAST_ERR_HEAD_DIM;
     const int64_t strides[10] = {kp_tok, kp_head, vp_tok, vp_head, ks_batch, ks_head, ks_tok, vs_batch, vs_head, vs_tok};
     for (int64_t s : strides)

@@ -468,9 +468,10 @@ __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, 
     return true;
 }
 
-template <int D, int WAVES, bool STORE>
+template <int D, int WAVES, bool STORE, typename E>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void tree_attn_mfma_kernel(AttnArgs a) {
+    using vec8 = typename E::vec8;
     constexpr int NT = WAVES * 64;
     constexpr int BN = 64;                 // keys per tile: two 32-key MFMA blocks
     constexpr int ROWS = WAVES * 32;       // query rows per workgroup
@@ -515,12 +516,12 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     const KvView<uint16_t> kv(a.kv, sq, h);
 
     // ---- Q^T operand (B side): query l32, head-dim slice [ds*16 + g*8, +8)
-    bf16x8 qreg[DSTEPS];
+    vec8 qreg[DSTEPS];
     {
         const uint16_t *src = qp + (int64_t)qtok * a.q_tok + (int64_t)qhead * a.q_head + g * 8;
 #pragma unroll
         for (int ds = 0; ds < DSTEPS; ++ds)
-            qreg[ds] = qvalid ? *reinterpret_cast<const bf16x8 *>(src + ds * 16) : bf16x8{};
+            qreg[ds] = qvalid ? *reinterpret_cast<const vec8 *>(src + ds * 16) : vec8{};
     }
     uint64_t mw0 = 0, mw1 = 0;
     if (qvalid && k_end > sq.S) {
@@ -640,9 +641,9 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             s[kb] = floatx16{};
 #pragma unroll
             for (int ds = 0; ds < DSTEPS; ++ds) {
-                const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(
+                const vec8 ka = *reinterpret_cast<const vec8 *>(
                     &Ks[buf][(kb * 32 + l32) * KPAD + ds * 16 + g * 8]);
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[ds], s[kb], 0, 0, 0);
+                s[kb] = E::mma(ka, qreg[ds], s[kb]);
             }
         }
         // issue order: the K operand reads run kQkAhead MFMAs ahead of
@@ -656,7 +657,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 0);
     };
     // visibility, the online softmax in base 2 and the P^T operand of tile t
-    auto softmax = [&](int t, floatx16 (&s)[2], bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+    auto softmax = [&](int t, floatx16 (&s)[2], vec8 (&pb)[2][2]) __attribute__((always_inline)) {
         // visibility (pack tiles and partial tiles only).  Element e of
         // lane (l32, g) in block kb is key t0 + 32*kb + 4*g + off(e),
         // off(e) = 8*(e/4) + e%4; in a pack tile that is pack key t0 - S + ...
@@ -709,8 +710,8 @@ void tree_attn_mfma_kernel(AttnArgs a) {
             for (int hf = 0; hf < 2; ++hf) {
                 u32x4 w;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[hf * 8 + 2 * e], p[hf * 8 + 2 * e + 1]);
-                pb[kb][hf] = __builtin_bit_cast(bf16x8, w);
+                for (int e = 0; e < 4; ++e) w[e] = E::pack2(p[hf * 8 + 2 * e], p[hf * 8 + 2 * e + 1]);
+                pb[kb][hf] = __builtin_bit_cast(vec8, w);
             }
         }
         lsum += acc;
@@ -718,16 +719,16 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     // O^T += V^T P^T over four 16-key slices.  Slot j of lane group g in
     // slice (kb, hf) is key 32*kb + 16*hf + 8*(j/4) + 4*g + j%4, stored at
     // column 32*kb + 16*hf + 8*g + j.
-    auto pv = [&](int buf, const bf16x8 (&pb)[2][2]) __attribute__((always_inline)) {
+    auto pv = [&](int buf, const vec8 (&pb)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int db = 0; db < DB; ++db) {
-                    const bf16x8 va = *reinterpret_cast<const bf16x8 *>(
+                    const vec8 va = *reinterpret_cast<const vec8 *>(
                         &Vt[buf][(db * 32 + l32) * VPAD + kb * 32 + hf * 16 + g * 8]);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb][hf], o[db], 0, 0, 0);
+                    o[db] = E::mma(va, pb[kb][hf], o[db]);
                 }
         // the same for the V^T operand reads of the PV product; the
         // exponentials stay free to fill the gaps
@@ -749,7 +750,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         if (t + 1 < ntiles) fetch(t + 1);
         if (!active) continue;
         floatx16 s[2];
-        bf16x8 pb[2][2];
+        vec8 pb[2][2];
         qk(buf, s);
         softmax(t, s, pb);
         pv(buf, pb);
@@ -770,8 +771,8 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const int d = db * 32 + 8 * r4 + 4 * g;
-                const u32x2 w = {pack_bf16x2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv),
-                                 pack_bf16x2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv)};
+                const u32x2 w = {E::pack2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv),
+                                 E::pack2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv)};
                 *reinterpret_cast<u32x2 *>(op + d) = w;
             }
         if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
@@ -1070,7 +1071,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
 // One workgroup per (packed token, group of query heads): a.comb_groups
 // groups of ceil(Hq / comb_groups) heads, each thread one 4-wide chunk of a
 // head's output at a time.
-template <typename OutT, int D>
+template <typename OutT, int D, typename E>   // E: the 16-bit format when OutT is 2 bytes
 __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     constexpr int C = D / 4;
     const int groups = a.comb_groups;
@@ -1111,7 +1112,7 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
         if (M != -INFINITY) acc *= 1.f / L;
         OutT *op = static_cast<OutT *>(a.out) + (int64_t)tok * a.o_tok + (int64_t)hq * a.o_head + d4 * 4;
         if constexpr (sizeof(OutT) == 2) {
-            const u32x2 w = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+            const u32x2 w = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
             *reinterpret_cast<u32x2 *>(op) = w;
         } else {
             *reinterpret_cast<floatx4 *>(op) = acc;
@@ -1235,14 +1236,16 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
 // DMAX sizes the LDS tiles: 128 (42 KB) for head_dim <= 128, 256 (83 KB)
 // above, as the reference kernel takes any power-of-two head_dim.
 // --------------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ float load_elem(const T *p);
-template <>
-__device__ __forceinline__ float load_elem<float>(const float *p) { return *p; }
-template <>
-__device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *p) { return bf16_to_float(*p); }
+template <typename T, typename E>
+__device__ __forceinline__ float load_elem(const T *p) {
+    if constexpr (sizeof(T) == 2)
+        return E::widen(*p);
+    else
+        return *p;
+}
 
-template <typename T, int DMAX>
+// T: float or uint16_t; E: the 16-bit format when T is 2 bytes
+template <typename T, int DMAX, typename E>
 __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int D) {
     constexpr int R = 16, BK = 32;
     __shared__ float Qs[R][DMAX];
@@ -1267,7 +1270,7 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
     const T *qp = static_cast<const T *>(a.q);
     const KvView<T> kv(a.kv, sq, h);
     for (int d = sub; d < D; d += 16)
-        Qs[row][d] = valid ? load_elem(qp + (int64_t)tok * a.q_tok + (int64_t)hq * a.q_head + d) : 0.f;
+        Qs[row][d] = valid ? load_elem<T, E>(qp + (int64_t)tok * a.q_tok + (int64_t)hq * a.q_head + d) : 0.f;
     uint64_t w0 = 0, w1 = 0;
     if (valid) {
         w0 = a.mask[(int64_t)tok * a.mask_words];
@@ -1284,8 +1287,8 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
             const int key = c / D, d = c % D;
             const int kk = t0 + key;
             const bool in = kk < sq.T;
-            Ks[key][d] = in ? load_elem(kv.key(kk, sq.S) + d) : 0.f;
-            Vs[key][d] = in ? load_elem(kv.val(kk, sq.S) + d) : 0.f;
+            Ks[key][d] = in ? load_elem<T, E>(kv.key(kk, sq.S) + d) : 0.f;
+            Vs[key][d] = in ? load_elem<T, E>(kv.val(kk, sq.S) + d) : 0.f;
         }
         __syncthreads();
         float sv[2];
@@ -1327,7 +1330,7 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
         if (d >= D) continue;
         const float x = acc[e] * inv;
         if constexpr (sizeof(T) == 2)
-            op[d] = (uint16_t)(pack_bf16x2(x, 0.f) & 0xffffu);
+            op[d] = (uint16_t)(E::pack2(x, 0.f) & 0xffffu);
         else
             op[d] = x;
     }
@@ -1339,7 +1342,7 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
 // Host side
 // --------------------------------------------------------------------------
 static bool mfma_path(int32_t dtype, int32_t D) {
-    return (dtype == CAST_BF16 || dtype == CAST_FP32) && (D == 64 || D == 128);
+    return (dtype == CAST_BF16 || dtype == CAST_FP16 || dtype == CAST_FP32) && (D == 64 || D == 128);
 }
 
 // Waves per workgroup (32 query rows each) for the largest possible pack.
@@ -1412,7 +1415,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
                          void *workspace, size_t workspace_bytes, int32_t *status, cast_stream_t stream, int stages) {
     if (batch < 0 || total_q < 0 || total_kv < 0 || head_dim <= 0) return CAST_ERR_SHAPE;
     if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return CAST_ERR_HEAD_RATIO;
-    if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
+    if (dtype != CAST_BF16 && dtype != CAST_FP16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
     if (mask_words != 1 && mask_words != 2) return CAST_ERR_SHAPE;
     if (kv.store && kv.cap < 0) return CAST_ERR_SHAPE;
     if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return CAST_ERR_SCALE;
@@ -1422,7 +1425,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         return CAST_ERR_NULL_POINTER;
     const bool mfma = mfma_path(dtype, head_dim);
     if (!mfma && (head_dim > 256 || head_dim % 8)) return CAST_ERR_HEAD_DIM;
-    const int64_t esz = dtype == CAST_BF16 ? 2 : 4;
+    const int64_t esz = dtype == CAST_FP32 ? 4 : 2;
     int32_t max_rows = INT32_MAX;
     auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (mfma) {
@@ -1479,14 +1482,18 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         const int64_t items = (int64_t)num_kv_heads * (((int64_t)total_q * a.G + 15) / 16 + batch);
         if (!(stages & kStageAttn)) return CAST_OK;
         const bool wide = head_dim > 128;
-        if (dtype == CAST_FP32 && wide)
-            tree_attn_generic_kernel<float, 256><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
-        else if (dtype == CAST_FP32)
-            tree_attn_generic_kernel<float, 128><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
-        else if (wide)
-            tree_attn_generic_kernel<uint16_t, 256><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
-        else
-            tree_attn_generic_kernel<uint16_t, 128><<<(unsigned)items, 256, 0, st>>>(a, head_dim);
+#define CAST_GENERIC(T, DM, E) tree_attn_generic_kernel<T, DM, E><<<(unsigned)items, 256, 0, st>>>(a, head_dim)
+        if (dtype == CAST_FP32) {
+            if (wide) CAST_GENERIC(float, 256, Bf16);
+            else CAST_GENERIC(float, 128, Bf16);
+        } else if (dtype == CAST_FP16) {
+            if (wide) CAST_GENERIC(uint16_t, 256, Fp16);
+            else CAST_GENERIC(uint16_t, 128, Fp16);
+        } else {
+            if (wide) CAST_GENERIC(uint16_t, 256, Bf16);
+            else CAST_GENERIC(uint16_t, 128, Bf16);
+        }
+#undef CAST_GENERIC
         return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
     }
 
@@ -1512,12 +1519,14 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     int64_t items = (int64_t)num_kv_heads * rbmax * nsplit;
     items = batch <= 64 ? sorted_slots((int64_t)num_kv_heads * nsplit, rbmax) : (items + 7) & ~(int64_t)7;
     const unsigned grid = (unsigned)items;
-#define CAST_LAUNCH(DD, W)                                                 \
-    (kv.store ? tree_attn_mfma_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
-              : tree_attn_mfma_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
+#define CAST_LAUNCH_E(DD, W, E)                                                \
+    (kv.store ? tree_attn_mfma_kernel<DD, W, true, E><<<grid, W * 64, 0, st>>>(a) \
+              : tree_attn_mfma_kernel<DD, W, false, E><<<grid, W * 64, 0, st>>>(a))
+#define CAST_LAUNCH(DD, W) (f16 ? CAST_LAUNCH_E(DD, W, Fp16) : CAST_LAUNCH_E(DD, W, Bf16))
 #define CAST_LAUNCH_F32(DD, W)                                                \
     (kv.store ? tree_attn_f32_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
               : tree_attn_f32_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
+    const bool f16 = dtype == CAST_FP16;
     if (!(stages & kStageAttn)) {
     } else if (dtype == CAST_FP32) {
         if (head_dim == 128) {
@@ -1537,6 +1546,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         else CAST_LAUNCH(64, 8);
     }
 #undef CAST_LAUNCH
+#undef CAST_LAUNCH_E
 #undef CAST_LAUNCH_F32
     if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     if (a.chunk != kNoSplit && (stages & kStageCombine)) {
@@ -1547,11 +1557,14 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         a.comb_groups = (int32_t)g;
         const unsigned cg = (unsigned)(total_q * g);
         if (dtype == CAST_FP32) {
-            if (head_dim == 128) tree_attn_combine_kernel<float, 128><<<cg, 256, 0, st>>>(a);
-            else tree_attn_combine_kernel<float, 64><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 128) tree_attn_combine_kernel<float, 128, Bf16><<<cg, 256, 0, st>>>(a);
+            else tree_attn_combine_kernel<float, 64, Bf16><<<cg, 256, 0, st>>>(a);
+        } else if (dtype == CAST_FP16) {
+            if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Fp16><<<cg, 256, 0, st>>>(a);
+            else tree_attn_combine_kernel<uint16_t, 64, Fp16><<<cg, 256, 0, st>>>(a);
         } else {
-            if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128><<<cg, 256, 0, st>>>(a);
-            else tree_attn_combine_kernel<uint16_t, 64><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Bf16><<<cg, 256, 0, st>>>(a);
+            else tree_attn_combine_kernel<uint16_t, 64, Bf16><<<cg, 256, 0, st>>>(a);
         }
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     }

@@ -25,6 +25,12 @@ LLAMA31_8B = dict(Hq=32, Hkv=8, D=128, vocab=128256)
 DRAFT_LEN = 15          # future positions scored by one drafter pass
 
 
+def torch_dtype(name):
+    """The torch dtype of a workload dtype name ("bf16", "fp16" or "fp32")."""
+    import torch
+    return {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[name]
+
+
 @dataclass
 class Workload:
     name: str
@@ -34,7 +40,7 @@ class Workload:
     Hq: int
     Hkv: int
     D: int
-    dtype: str                  # "bf16" | "fp32"
+    dtype: str                  # "bf16" | "fp16" | "fp32"
     vocab: int
     qkv_scale: float = 1.0
     seed: int = 0
@@ -72,7 +78,7 @@ class Workload:
         K and V once per KV head, Q read and O written once, LSE written,
         the ancestor words read once.
         """
-        e = elem or (2 if self.dtype == "bf16" else 4)
+        e = elem or (4 if self.dtype == "fp32" else 2)
         S = self.prefix_len.astype(np.int64)
         P = self.pack_len.astype(np.int64)
         kv = int(((S + P) * self.Hkv * self.D * e * 2).sum())
@@ -93,7 +99,7 @@ class Workload:
     def qkv(self, device="cpu", generator_device="cpu"):
         """Seeded q [total_q,Hq,D], k/v [total_kv,Hkv,D] in the workload dtype."""
         import torch
-        dt = torch.bfloat16 if self.dtype == "bf16" else torch.float32
+        dt = torch_dtype(self.dtype)
         g = torch.Generator(device=generator_device).manual_seed(self.seed)
 
         def draw(*shape):
@@ -232,7 +238,7 @@ def planted_logits(workload, vocab=None, seed=0, accept_p=0.8, device="cpu", dty
     V = vocab or workload.vocab
     if int(workload.packed.token.max(initial=0)) >= V:
         raise ValueError("tree tokens must be smaller than the logits vocabulary")
-    dt = dtype or (torch.bfloat16 if workload.dtype == "bf16" else torch.float32)
+    dt = dtype or torch_dtype(workload.dtype)
     rng = np.random.default_rng(seed + 7919)
     g = torch.Generator(device=generator_device).manual_seed(seed + 104729)
     logits = torch.randn(workload.total_q, V, generator=g, device=generator_device,

@@ -443,7 +443,7 @@ def _tree_attention(module, query, key, value, attention_mask, scaling=None, dro
     (prefill, no mask, a non-tree mask) runs plain SDPA."""
     meta = None
     if (isinstance(attention_mask, torch.Tensor) and query.shape[0] == 1 and query.is_cuda
-            and query.dtype in (torch.bfloat16, torch.float32)):
+            and query.dtype in (torch.bfloat16, torch.float16, torch.float32)):
         meta = _tree_meta(attention_mask, int(key.shape[2]))
     if meta is None:
         return _plain_attention(query, key, value, attention_mask, scaling)

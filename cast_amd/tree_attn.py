@@ -34,7 +34,7 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.bfloat16: _lib.BF16, torch.float32: _lib.FP32}
+_DTYPES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16, torch.float32: _lib.FP32}
 
 
 def _as_i32(x, device):
@@ -149,7 +149,7 @@ def varlen_tree_attention(q, k, v, cu_q, cu_kv, prefix_len, pack_len, ancestor_m
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     if q.dtype not in _DTYPES:
-        raise ValueError(f"unsupported dtype {q.dtype}: use bfloat16 or float32")
+        raise ValueError(f"unsupported dtype {q.dtype}: use bfloat16, float16 or float32")
     if k.dtype != q.dtype:
         k = k.to(q.dtype)
     if v.dtype != q.dtype:
@@ -233,7 +233,7 @@ def store_tree_attention(q, k_store, v_store, k_pack, v_pack, cu_q, prefix_len, 
     if tuple(k_pack.shape) != (H_kv, total_q, D) or tuple(v_pack.shape) != (H_kv, total_q, D):
         raise ValueError(f"k_pack/v_pack must be [{H_kv}, {total_q}, {D}]")
     if q.dtype not in _DTYPES:
-        raise ValueError(f"unsupported dtype {q.dtype}: use bfloat16 or float32")
+        raise ValueError(f"unsupported dtype {q.dtype}: use bfloat16, float16 or float32")
     if any(t.dtype != q.dtype for t in (k_store, v_store, k_pack, v_pack)):
         raise ValueError("q, the store and the pack K/V must share one dtype (the store is read in place)")
     if sm_scale is None:

@@ -64,7 +64,8 @@ def tree_bitmask(parent, cu_q, words=2, *, check=False):
 def greedy_accept(logits, cu_q, parent, token, *, check=False):
     """Greedy accepted paths of a packed batch, without host synchronisation.
 
-    logits: [total_q, V] bf16/fp32 on the device (row r = packed row r);
+    logits: [total_q, V] bf16/fp16/fp32 on the device (row r = packed row r;
+    other float dtypes are widened to fp32 first);
     cu_q int32 [B+1]; parent int32 [total_q] pack-local; token int64
     [total_q] draft tokens (the root's entry is ignored).  Returns device
     tensors (path int32 [B,128] of node indices, -1 padded; path_len int32
@@ -74,7 +75,7 @@ def greedy_accept(logits, cu_q, parent, token, *, check=False):
     if not logits.is_cuda:
         raise ValueError("greedy_accept runs on the GPU: logits must be a device tensor")
     dev = logits.device
-    if logits.dtype not in (torch.bfloat16, torch.float32):
+    if logits.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         logits = logits.float()
     if logits.dim() != 2:
         raise ValueError("logits must be [total_q, V]")
@@ -92,7 +93,7 @@ def greedy_accept(logits, cu_q, parent, token, *, check=False):
     bonus = torch.empty(B, dtype=torch.int64, device=dev)
     argmax = torch.empty(total_q, dtype=torch.int32, device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if check else None
-    dt = _lib.BF16 if logits.dtype == torch.bfloat16 else _lib.FP32
+    dt = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}.get(logits.dtype, _lib.FP32)
     with _lib.on_device(dev):
         st = lib.cast_greedy_accept(_lib.ptr(logits), logits.stride(0), V, dt, _lib.ptr(cu_q), _lib.ptr(parent),
                                     _lib.ptr(token), B, total_q, _lib.ptr(argmax), _lib.ptr(path),

@@ -55,7 +55,7 @@ enum cast_device_flag {
                                       rows and 2^31 bytes per source) */
 };
 
-enum cast_dtype { CAST_BF16 = 0, CAST_FP32 = 1, CAST_FP64 = 2 };
+enum cast_dtype { CAST_BF16 = 0, CAST_FP32 = 1, CAST_FP64 = 2, CAST_FP16 = 3 };
 
 /* Library ABI version (bumped on any signature change). */
 int cast_abi_version(void);

@@ -115,7 +115,8 @@ def test_store_append_host_validation(lib):
         [None] * 3 + [o.get("B", 2), 16, 64, 4, 128] + [8] * 10 + [o.get("dtype", 0), None, None]
     assert f(*args()) == 1                       # null pointers
     assert f(*args(stride=64)) == 7              # path rows narrower than 128
-    assert f(*args(dtype=3)) == 4                # dtype
+    assert f(*args(dtype=2)) == 4                # dtype (fp64 has no row copy)
+    assert f(*args(dtype=9)) == 4
     assert f(*args(B=0)) == 0 and f(*args(layers=0)) == 0
 
 

@@ -36,10 +36,10 @@ def _setup(dev, seed, B=5, L=3, Hkv=4, D=128, cap=96, dtype=torch.bfloat16):
     return buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted
 
 
-@pytest.mark.parametrize("case", ["all-rows", "compact", "grow", "fp32-d64"])
+@pytest.mark.parametrize("case", ["all-rows", "compact", "grow", "fp32-d64", "fp16"])
 def test_append_store_matches_reference(gpu, case):
     from cast_amd import serving
-    kw = dict(D=64, dtype=torch.float32) if case == "fp32-d64" else {}
+    kw = {"fp32-d64": dict(D=64, dtype=torch.float32), "fp16": dict(dtype=torch.float16)}.get(case, {})
     buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=len(case), **kw)
     B = len(store_len)
     rows = [0, 2, 3] if case == "compact" else list(range(B))

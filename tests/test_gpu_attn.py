@@ -17,7 +17,8 @@ from oracle import bitmask as OB
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"bf16": dict(out=2e-2, lse=1e-3, mean=2e-3), "fp32": dict(out=1e-4, lse=1e-4, mean=1e-5)}
+TOL = {"bf16": dict(out=2e-2, lse=1e-3, mean=2e-3), "fp16": dict(out=5e-3, lse=1e-3, mean=5e-4),
+       "fp32": dict(out=1e-4, lse=1e-4, mean=1e-5)}
 
 
 def _words(wl):
@@ -106,6 +107,23 @@ def test_gqa_ratios_and_head_dim_64(gpu):
         wl = SC.random_parent_batch(seed=Hq + D, B=3, Hq=Hq, Hkv=Hkv, D=D, s_lo=50, s_hi=700, p_lo=1, p_hi=129,
                                     dtype=dt, qkv_scale=0.5)
         _run_and_check(wl, gpu, label=f"gqa{Hq}/{Hkv}-D{D}-{dt}")
+
+
+def test_fp16_inputs(gpu):
+    # the reference kernel runs on fp16 tensors as well (its tl.dot and
+    # empty_like follow q's dtype): the MFMA kernels (f16 products, P rounded
+    # to fp16), the split-K combine writing fp16, and the scalar kernel
+    wl = SC.random_parent_batch(seed=0, dtype="fp16")
+    _run_and_check(wl, gpu, label="reference-scenario-fp16")
+    _run_and_check(wl, gpu, one_word=True, label="reference-scenario-fp16-int64-mask")
+    wl = SC.random_parent_batch(seed=4, B=4, Hq=16, Hkv=4, D=64, s_lo=200, s_hi=3000, p_lo=1, p_hi=129,
+                                dtype="fp16", qkv_scale=0.5)
+    for split in (0, 128, -1):
+        _run_and_check(wl, gpu, kv_split=split, label=f"fp16-d64-split{split}")
+    for D in (96, 256):
+        wl = SC.random_parent_batch(seed=D, B=3, Hq=8, Hkv=2, D=D, s_lo=20, s_hi=300, p_lo=1, p_hi=129,
+                                    dtype="fp16", qkv_scale=0.5)
+        _run_and_check(wl, gpu, label=f"fp16-scalar-d{D}")
 
 
 def test_head_dims_above_128(gpu):

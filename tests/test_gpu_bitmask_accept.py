@@ -168,3 +168,38 @@ def test_bf16_argmax_edge_rows(gpu, V):
     dev = wide.to(gpu)[:, :V]
     assert dev.stride(0) == V + 3
     assert np.array_equal(_argmax_rows(gpu, dev), want)
+
+
+def _f16_bits(bits):
+    return torch.tensor([bits - 65536 if bits >= 32768 else bits], dtype=torch.int16).view(torch.float16)[0]
+
+
+@pytest.mark.parametrize("V", [151936, 1001])
+def test_fp16_argmax_edge_rows(gpu, V):
+    # fp16 logits take the same 16-bit order keys with fp16's infinity
+    # (0x7c00) as the NaN bound: signed zeros, infinities, denormals, NaNs of
+    # either sign (quiet and signalling patterns), ties, the last element
+    g = torch.Generator().manual_seed(V + 1)
+    rows = []
+    def row(fill):
+        return torch.full((V,), fill, dtype=torch.float16)
+    r = row(-0.0); r[V // 2] = 0.0; rows.append(r)
+    rows.append(-(torch.rand(V, generator=g) + 0.5).half())
+    r = torch.randn(V, generator=g).half(); r[V // 3] = float("inf"); r[V // 5] = float("inf"); rows.append(r)
+    r = row(float("-inf")); r[V - 7] = -6e4; rows.append(r)
+    rows.append(row(float("-inf")))
+    r = torch.randint(1, 1023, (V,), generator=g, dtype=torch.int16); r[V - 3] = 1023
+    rows.append(r.view(torch.float16))                                     # positive denormals
+    r = torch.randn(V, generator=g).half(); r[V // 2] = float("nan"); r[3] = 6e4; rows.append(r)
+    r = torch.randn(V, generator=g).half(); r[V // 4] = _f16_bits(0xFE00); rows.append(r)     # negative NaN
+    r = torch.randn(V, generator=g).half(); r[2 * V // 3] = _f16_bits(0x7C01); rows.append(r)  # signalling NaN
+    r = torch.randn(V, generator=g).half(); r[17] = 7.0; r[16] = 7.0; r[V - 1] = 7.0; rows.append(r)
+    r = torch.randn(V, generator=g).half(); r[V - 1] = 9.0; rows.append(r)
+    r = torch.randint(-2, 3, (V,), generator=g).half(); rows.append(r)
+    logits = torch.stack(rows)
+    print(f"case fp16-argmax-edges V={V}: {logits.shape[0]} rows", flush=True)
+    want = OW.row_argmax_all(logits)
+    assert np.array_equal(_argmax_rows(gpu, logits.to(gpu)), want)
+    wide = torch.cat([logits, logits[:, :3]], dim=1)
+    dev = wide.to(gpu)[:, :V]
+    assert np.array_equal(_argmax_rows(gpu, dev), want)

@@ -22,7 +22,8 @@ from oracle import bitmask as OB
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"bf16": dict(out=2e-2, lse=1e-3, mean=2e-3), "fp32": dict(out=1e-4, lse=1e-4, mean=1e-5)}
+TOL = {"bf16": dict(out=2e-2, lse=1e-3, mean=2e-3), "fp16": dict(out=5e-3, lse=1e-3, mean=5e-4),
+       "fp32": dict(out=1e-4, lse=1e-4, mean=1e-5)}
 
 
 def _to_store(wl, q, k, v, dev, extra=37):
@@ -74,12 +75,13 @@ def _check_store(wl, dev, kv_split=0, requests=None, label=""):
     assert err_o.max() <= tol["out"] and err_o.mean() <= tol["mean"] and err_l.max() <= tol["lse"]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
 def test_store_reference_scenario(gpu, dtype):
     _check_store(SC.random_parent_batch(seed=1, dtype=dtype), gpu, label=f"store-reference-scenario-{dtype}")
 
 
-@pytest.mark.parametrize("dtype,B,kv_split", [("bf16", 4, 0), ("fp32", 4, 128), ("bf16", 70, 0), ("fp32", 70, -1)])
+@pytest.mark.parametrize("dtype,B,kv_split", [("bf16", 4, 0), ("fp32", 4, 128), ("bf16", 70, 0), ("fp32", 70, -1),
+                                              ("fp16", 4, 128), ("fp16", 70, 0)])
 def test_store_head_dim_64_and_large_batches(gpu, dtype, B, kv_split):
     # D = 64 instances and batches past 64 requests (batch-order schedule) in the store layout
     wl = SC.random_parent_batch(seed=B + 3, B=B, Hq=16, Hkv=4, D=64, s_lo=30, s_hi=600, p_lo=1, p_hi=90,
