@@ -91,7 +91,7 @@ int cast_tree_bitmask(const int32_t *parent, const int32_t *cu_q, int32_t batch,
  *   cu_q, cu_kv  int32 [batch+1];  prefix_len, pack_len  int32 [batch]
  *   mask   uint64 [total_q][mask_words], mask_words 1 (int64 reference
  *          layout) or 2
- *   dtype  cast_dtype of q, k, v and out
+ *   dtype  cast_dtype of q, k, v and out: CAST_BF16, CAST_FP16 or CAST_FP32
  *   head_dim  64 or 128 on the MFMA kernels; any other multiple of 8 up to
  *          256 on a scalar kernel (the reference takes any power of two)
  *   sm_scale  > 0 (the Python layer substitutes 1/sqrt(D) for None)
@@ -215,7 +215,8 @@ int32_t cast_tree_attn_default_split(int32_t batch, int32_t total_q, int32_t tot
  * Replaces the temperature-0 walk of cast_trees/decode.py:85-103 (pick at
  * decode.py:13-15) called per request at cast_trees/serving.py:326-335.
  *   logits   [total_q, vocab], row stride logits_ld elements, dtype
- *            CAST_BF16 or CAST_FP32; packed row r = pack row (root first)
+ *            CAST_BF16, CAST_FP16 or CAST_FP32; packed row r = pack row
+ *            (root first)
  *   cu_q     int32 [batch+1];  parent int32 [total_q] pack-local (-1 root)
  *   token    int64 [total_q]  draft token of every packed row (root ignored)
  *   argmax   int32 [total_q]  out: first index of each row's maximum
@@ -272,6 +273,7 @@ int cast_store_append(const void *const *k_pack, const void *const *v_pack, void
  * cast_draft_topk replaces topk_marginals (cast_trees/verify.py:8-12; the
  * log_softmax + topk + .cpu() of cast_trees/serving.py:126-128):
  *   logits   [rows, vocab] bf16 / fp32, row stride logits_ld elements
+ *            (fp16 logits: widen to fp32 first)
  *   top_idx  int64 [rows][k] token ids, top_lp  float [rows][k] log-probs,
  *            ranked by descending log-probability, equal values in
  *            increasing index order (cast_trees/tree.py:20-26); 1 <= k <= 16,
