@@ -500,17 +500,18 @@ def bitmask_lines(dev, steps, warmup):
 
 
 ATTN_WORKLOADS = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
-                  "qwen3-8b-stress-b32", "qwen3-8b-b8-ctx8k-p128-fp32")
+                  "qwen3-8b-stress-b32", "qwen3-8b-b8-ctx8k-p128-fp32", "qwen3-8b-b8-ctx8k-p128-fp16")
 
 
 def attn_workload(dev, name, steps, warmup):
     """One attention workload timed like the headline (2 rotated K/V sets)."""
     import torch
     from cast_amd import scenarios
-    if name.endswith("-fp32"):
-        # the headline shapes in fp32: what the unchanged reference hook
-        # hands the kernel (cast_trees/serving.py:68-71)
-        wl = dataclasses.replace(scenarios.CONFIGS[name[:-5]](), dtype="fp32", name=name)
+    if name.endswith(("-fp32", "-fp16")):
+        # the headline shapes in fp32 (what the unchanged reference hook hands
+        # the kernel, cast_trees/serving.py:68-71) or in fp16 (same MFMA rate
+        # as bf16 on this part)
+        wl = dataclasses.replace(scenarios.CONFIGS[name[:-5]](), dtype=name[-4:], name=name)
     else:
         wl = scenarios.CONFIGS[name]()
     h = Harness(wl, dev, sets=2, kv_split=0)
@@ -764,9 +765,10 @@ def main():
         "algorithmic_bytes": wl.algorithmic_bytes(), "algorithmic_flops": wl.algorithmic_flops(),
     }
     # the practical MFMA ceiling of this launch shape, timed right after the
-    # headline calls (same clock state): the headline's MFMA count with LDS
-    # operand reads and the per-tile barrier, no softmax and no loads
-    ceil = CeilingLoop(dev).run(3, args.steps, min(args.warmup, 5))
+    # headline calls with the same step and warmup counts: the headline's MFMA
+    # count with LDS operand reads and the per-tile barrier, no softmax and no
+    # loads.  Its clock depends on the load before it, as the kernel's does.
+    ceil = CeilingLoop(dev).run(3, args.steps, args.warmup)
     ceil["attention_frac_of_ceiling"] = round(rl["achieved"] / ceil["tflops"], 4)
     ceil["loop"] = "lds_operands_barrier"
     line["mfma_ceiling"] = ceil
