@@ -469,8 +469,12 @@ __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, 
     return true;
 }
 
-template <int D, int WAVES, bool STORE, typename E>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+// WPE: waves per SIMD the register budget is sized for.  2 (256 registers a
+// lane) for head_dim 64 and 128; 1 (512) for head_dim 256, whose O^T
+// accumulators (128 registers), Q^T operand (64), scores and staged K/V
+// tiles take about 330.
+template <int D, int WAVES, bool STORE, typename E, int WPE = 2>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void tree_attn_mfma_kernel(AttnArgs a) {
     using vec8 = typename E::vec8;
     constexpr int NT = WAVES * 64;
@@ -1343,15 +1347,19 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
 // Host side
 // --------------------------------------------------------------------------
 static bool mfma_path(int32_t dtype, int32_t D) {
-    return (dtype == CAST_BF16 || dtype == CAST_FP16 || dtype == CAST_FP32) && (D == 64 || D == 128);
+    if (dtype == CAST_FP32) return D == 64 || D == 128;
+    return (dtype == CAST_BF16 || dtype == CAST_FP16) && (D == 64 || D == 128 || D == 256);
 }
 
 // Waves per workgroup (32 query rows each) for the largest possible pack.
 // (The fp32 kernel has no 2-wave instance: its staging registers would not
 // fit beside the Q and O operands.)
-static int waves_for(int32_t total_q, int32_t G, int32_t dtype) {
+// Head_dim 256 always runs 4 waves, one per SIMD: fewer threads would each
+// stage more of its 32 KB tiles than the registers hold.
+static int waves_for(int32_t total_q, int32_t G, int32_t dtype, int32_t D) {
     const int pmax = total_q < kMaxPack ? total_q : kMaxPack;
     const int rows = pmax * G;
+    if (D == 256) return 4;
     const int w = rows <= 64 ? 2 : rows <= 128 ? 4 : 8;
     return dtype == CAST_FP32 && w < 4 ? 4 : w;
 }
@@ -1361,7 +1369,7 @@ static int32_t resolve_chunk(int32_t batch, int32_t total_q, int32_t total_kv, i
     if (!mfma_path(dtype, D) || kv_split < 0 || batch <= 0) return kNoSplit;
     if (kv_split > 0) return ((kv_split + 63) / 64) * 64;
     const int G = Hq / Hkv;
-    const int rows_wg = waves_for(total_q, G, dtype) * 32;
+    const int rows_wg = waves_for(total_q, G, dtype, D) * 32;
     const int64_t p_avg = (total_q + batch - 1) / batch;
     const int64_t p_est = p_avg < kMaxPack ? p_avg : kMaxPack;
     const int64_t rb = (p_est * G + rows_wg - 1) / rows_wg;
@@ -1498,7 +1506,7 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
         return hipGetLastError() == hipSuccess ? CAST_OK : CAST_ERR_HIP;
     }
 
-    const int waves = waves_for(total_q, a.G, dtype);
+    const int waves = waves_for(total_q, a.G, dtype, head_dim);
     a.rows_wg = waves * 32;
     a.chunk = resolve_chunk(batch, total_q, total_kv, num_q_heads, num_kv_heads, head_dim, dtype, kv_split);
     if (a.chunk != kNoSplit) {
@@ -1524,6 +1532,10 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     (kv.store ? tree_attn_mfma_kernel<DD, W, true, E><<<grid, W * 64, 0, st>>>(a) \
               : tree_attn_mfma_kernel<DD, W, false, E><<<grid, W * 64, 0, st>>>(a))
 #define CAST_LAUNCH(DD, W) (f16 ? CAST_LAUNCH_E(DD, W, Fp16) : CAST_LAUNCH_E(DD, W, Bf16))
+#define CAST_LAUNCH_WIDE_E(W, E)                                                       \
+    (kv.store ? tree_attn_mfma_kernel<256, W, true, E, 1><<<grid, W * 64, 0, st>>>(a) \
+              : tree_attn_mfma_kernel<256, W, false, E, 1><<<grid, W * 64, 0, st>>>(a))
+#define CAST_LAUNCH_WIDE(W) (f16 ? CAST_LAUNCH_WIDE_E(W, Fp16) : CAST_LAUNCH_WIDE_E(W, Bf16))
 #define CAST_LAUNCH_F32(DD, W)                                                \
     (kv.store ? tree_attn_f32_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
               : tree_attn_f32_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
@@ -1537,6 +1549,8 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
             if (waves == 4) CAST_LAUNCH_F32(64, 4);
             else CAST_LAUNCH_F32(64, 8);
         }
+    } else if (head_dim == 256) {
+        CAST_LAUNCH_WIDE(4);
     } else if (head_dim == 128) {
         if (waves == 2) CAST_LAUNCH(128, 2);
         else if (waves == 4) CAST_LAUNCH(128, 4);
@@ -1548,6 +1562,8 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     }
 #undef CAST_LAUNCH
 #undef CAST_LAUNCH_E
+#undef CAST_LAUNCH_WIDE
+#undef CAST_LAUNCH_WIDE_E
 #undef CAST_LAUNCH_F32
     if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     if (a.chunk != kNoSplit && (stages & kStageCombine)) {
@@ -1561,10 +1577,12 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
             if (head_dim == 128) tree_attn_combine_kernel<float, 128, Bf16><<<cg, 256, 0, st>>>(a);
             else tree_attn_combine_kernel<float, 64, Bf16><<<cg, 256, 0, st>>>(a);
         } else if (dtype == CAST_FP16) {
-            if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Fp16><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Fp16><<<cg, 256, 0, st>>>(a);
+            else if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Fp16><<<cg, 256, 0, st>>>(a);
             else tree_attn_combine_kernel<uint16_t, 64, Fp16><<<cg, 256, 0, st>>>(a);
         } else {
-            if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Bf16><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Bf16><<<cg, 256, 0, st>>>(a);
+            else if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Bf16><<<cg, 256, 0, st>>>(a);
             else tree_attn_combine_kernel<uint16_t, 64, Bf16><<<cg, 256, 0, st>>>(a);
         }
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;

@@ -128,11 +128,18 @@ def test_fp16_inputs(gpu):
 
 def test_head_dims_above_128(gpu):
     # the reference kernel takes any power-of-two head_dim (tl.arange(0, D),
-    # tree_attn.py:36); here 192 and 256 run on the scalar kernel's wide tiles
+    # tree_attn.py:36): 256 in bf16/fp16 runs the MFMA kernel at one wave per
+    # SIMD; fp32 at 256 and the other multiples of 8 take the scalar kernel
     for Hq, Hkv, D, dt in [(8, 2, 256, "bf16"), (4, 4, 256, "fp32"), (8, 4, 192, "bf16"), (4, 1, 136, "fp32")]:
         wl = SC.random_parent_batch(seed=D + Hq, B=3, Hq=Hq, Hkv=Hkv, D=D, s_lo=20, s_hi=300, p_lo=1, p_hi=129,
                                     dtype=dt, qkv_scale=0.5)
         _run_and_check(wl, gpu, label=f"head-dim-{D}-{Hq}/{Hkv}-{dt}")
+    # head_dim 256 on MFMA: long prefixes, split-K and the combine, both formats
+    for dt in ("bf16", "fp16"):
+        wl = SC.random_parent_batch(seed=7, B=4, Hq=16, Hkv=8, D=256, s_lo=500, s_hi=4000, p_lo=1, p_hi=129,
+                                    dtype=dt, qkv_scale=0.5)
+        for split in (0, 256, -1):
+            _run_and_check(wl, gpu, kv_split=split, label=f"head-dim-256-mfma-{dt}-split{split}")
 
 
 @pytest.mark.parametrize("B,dtype,kv_split", [(64, "bf16", 0), (65, "bf16", 0), (65, "bf16", 192),
