@@ -10,7 +10,7 @@
 // Work unit: (request b, KV head h, key split s, row block rb).  The Q rows of
 // a unit are the pack's tokens times the GQA group (row r = token*G + g), so
 // one KV head's keys are streamed from HBM once per split and shared by
-// G*P_b query rows.  bf16 or fp16 with head_dim 64/128 runs on MFMA:
+// G*P_b query rows.  bf16 or fp16 with head_dim 64/128/256 runs on MFMA:
 //   S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (_f16 for fp16 inputs; keys
 //   on the M side, queries on the N side, so each lane ends up owning one
 //   query column), then
@@ -18,7 +18,8 @@
 //   S^T accumulator registers (a lane's 16 score values are exactly the 8+8
 //   k-slots it must supply), V^T read from a transposed LDS copy.  fp32
 //   inputs run the same structure on v_mfma_f32_32x32x2_f32
-//   (tree_attn_f32_kernel); other head dims (up to 256) take a scalar kernel.
+//   (tree_attn_f32_kernel); other head dims (up to 256) take a scalar
+//   kernel.  Head_dim 256 runs one wave per SIMD (512 registers a lane).
 // K/V tiles of 64 keys are double-buffered through LDS with 16-byte loads;
 // the ancestor words are only consulted on the tile(s) holding pack keys.
 // The online softmax works in base 2 with a lazy rescale: the running max
