@@ -16,11 +16,14 @@ from oracle import bitmask as OB
 pytestmark = pytest.mark.gpu
 
 
+_DT = {"bf16": _lib.BF16, "fp16": _lib.FP16, "fp32": _lib.FP32}
+
+
 def _args(wl, dev, q, k, v, out, lse, mask, meta, kv_split):
     return [_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(meta["cu_q"]),
             _lib.ptr(meta["cu_kv"]), _lib.ptr(meta["prefix_len"]), _lib.ptr(meta["pack_len"]), _lib.ptr(mask), 2,
             wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, q.stride(0), q.stride(1), k.stride(0), k.stride(1),
-            v.stride(0), v.stride(1), out.stride(0), out.stride(1), _lib.BF16, float(wl.D ** -0.5), kv_split]
+            v.stride(0), v.stride(1), out.stride(0), out.stride(1), _DT[wl.dtype], float(wl.D ** -0.5), kv_split]
 
 
 def _both(gpu, wl, kv_split=0):
@@ -28,7 +31,7 @@ def _both(gpu, wl, kv_split=0):
     q, k, v = wl.qkv(device=gpu)
     meta = wl.meta_tensors(gpu)
     mask = torch.from_numpy(OB.chain_walk_words(wl.packed.parent, wl.cu_q).view(np.int64).copy()).to(gpu)
-    need = lib.cast_tree_attn_workspace_size(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, _lib.BF16,
+    need = lib.cast_tree_attn_workspace_size(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, _DT[wl.dtype],
                                              kv_split)
     print(f"case noalloc {wl.name}: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv} scratch {need} B",
           flush=True)
@@ -61,3 +64,11 @@ def test_noalloc_matches_workspace_entry_twice(gpu):
 def test_noalloc_headline_shapes(gpu):
     # the benchmark's shapes: 48 MiB of partials, within the 64 MiB array
     _both(gpu, SC.qwen3_headline(), kv_split=0)
+
+
+def test_noalloc_fp16_and_head_dim_256(gpu):
+    # the other element format and the one-wave-per-SIMD instance share the
+    # static scratch array the same way
+    for D in (128, 256):
+        _both(gpu, SC.random_parent_batch(seed=D, B=3, Hq=16, Hkv=8, D=D, s_lo=300, s_hi=3000, p_lo=1, p_hi=129,
+                                          dtype="fp16", qkv_scale=0.5), kv_split=256)
