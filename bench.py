@@ -500,7 +500,8 @@ def bitmask_lines(dev, steps, warmup):
 
 
 ATTN_WORKLOADS = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
-                  "qwen3-8b-stress-b32", "qwen3-8b-b8-ctx8k-p128-fp32", "qwen3-8b-b8-ctx8k-p128-fp16")
+                  "qwen3-8b-stress-b32", "qwen3-8b-b8-ctx8k-p128-fp32", "qwen3-8b-b8-ctx8k-p128-fp16",
+                  "d256-b8-ctx8k-p128")
 
 
 def attn_workload(dev, name, steps, warmup):

@@ -22,6 +22,7 @@ from .tree import PackedTrees, block_topk, build_chain, build_tree, pack_trees
 
 QWEN3_8B = dict(Hq=32, Hkv=8, D=128, vocab=151936)
 LLAMA31_8B = dict(Hq=32, Hkv=8, D=128, vocab=128256)
+HEADS_D256 = dict(Hq=16, Hkv=8, D=256, vocab=151936)   # 16 query / 8 KV heads of head_dim 256
 DRAFT_LEN = 15          # future positions scored by one drafter pass
 
 
@@ -181,6 +182,14 @@ def llama_long(seed=0, prefix=32768, pack=128):
                  1 / math.sqrt(128))
 
 
+def head_dim_256(seed=0, B=8, prefix=8192, pack=128):
+    """The headline batch with 16 query / 8 KV heads of head_dim 256 (the same
+    FLOPs per call), bf16: the one-wave-per-SIMD MFMA instance."""
+    rng = np.random.default_rng(seed)
+    trees = [_tree_from_scores(rng, pack, 5.0) for _ in range(B)]
+    return _make("d256-b8-ctx8k-p128", trees, [prefix] * B, HEADS_D256, "bf16", seed, 1 / math.sqrt(256))
+
+
 def stress_mixed(seed=0, B=32, lo=256, hi=4096, pack=128):
     """B=32, prefixes U[256,4k], P=128 each; even requests use deep/narrow
     trees (scores N(0,10)), odd ones wide trees (scores N(0,2))."""
@@ -219,6 +228,7 @@ CONFIGS = {
     "qwen3-8b-b8-ctx8k-p128": qwen3_headline,
     "llama31-8b-ctx32k-p128": llama_long,
     "qwen3-8b-stress-b32": stress_mixed,
+    "d256-b8-ctx8k-p128": head_dim_256,
 }
 
 
