@@ -400,7 +400,8 @@ __device__ __forceinline__ bool pack_bit(int j, uint64_t w0, uint64_t w1) {
 }
 
 // --------------------------------------------------------------------------
-// MFMA kernel: bf16, head_dim D in {64, 128}, WAVES waves x 32 query rows.
+// MFMA kernel: bf16 or fp16, head_dim D in {64, 128, 256}, WAVES waves x 32
+// query rows.
 // --------------------------------------------------------------------------
 
 // Bits [j0, j0+32) of the 192-bit string {w1 : w0 : 64 ones}, read from bit
@@ -1237,7 +1238,7 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
 }
 
 // --------------------------------------------------------------------------
-// Generic kernel: fp32 or bf16 inputs, any head_dim <= 256 (multiple of 8),
+// Generic kernel: fp32, bf16 or fp16 inputs, any head_dim <= 256 (multiple of 8),
 // scalar FMA.  One workgroup = 16 query rows of one (request, KV head).
 // DMAX sizes the LDS tiles: 128 (42 KB) for head_dim <= 128, 256 (83 KB)
 // above, as the reference kernel takes any power-of-two head_dim.
