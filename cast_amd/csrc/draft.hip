@@ -20,10 +20,11 @@ namespace cast {
 
 constexpr int kTopKMax = 16;
 
-template <bool BF16>
+// BF16: 16-bit elements, of format E (Bf16 or Fp16); else float.
+template <bool BF16, typename E = Bf16>
 __device__ __forceinline__ float logit_at(const char *row, int i) {
     if constexpr (BF16)
-        return bf16_to_float(reinterpret_cast<const uint16_t *>(row)[i]);
+        return E::widen(reinterpret_cast<const uint16_t *>(row)[i]);
     else
         return reinterpret_cast<const float *>(row)[i];
 }
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(64) void draft_topk_combine_kernel(const TopkPart *
 // Log-sum-exp: a running max per thread; a chunk's exp terms are summed
 // pairwise in float onto the thread's float sum, which is rescaled only when
 // the running max moves.  Workgroup and split sums are combined in double.
-template <bool BF16, int K>
+template <bool BF16, int K, typename E = Bf16>
 __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restrict__ logits, int64_t ld,
                                                              int32_t vocab, int32_t k, int32_t per_e,
                                                              TopkPart *__restrict__ part,
@@ -222,8 +223,11 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
             const uint32_t bits = w[BF16 ? (e >> 1) : e];
-            v[e] = BF16 ? __builtin_bit_cast(float, (e & 1) ? (bits & 0xffff0000u) : (bits << 16))
-                        : __builtin_bit_cast(float, bits);
+            if constexpr (BF16 && __is_same(E, Fp16))
+                v[e] = f16_to_float((uint16_t)(bits >> ((e & 1) * 16)));
+            else
+                v[e] = BF16 ? __builtin_bit_cast(float, (e & 1) ? (bits & 0xffff0000u) : (bits << 16))
+                            : __builtin_bit_cast(float, bits);
         }
     };
     auto chunk_max = [&](const float (&v)[EPC]) __attribute__((always_inline)) {
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(kTopkNT) void draft_topk_kernel(const void *__restr
             if (c + u * NT < ce) chunk(w[u], c + u * NT);
     }
     for (int i = tail0 + tid; i < e1; i += NT) {
-        const float v[1] = {logit_at<BF16>(base, i)};
+        const float v[1] = {logit_at<BF16, E>(base, i)};
         lse_add(v, v[0]);
         const uint64_t key = rank_key(v[0], i);
         if (key >= thr) insert(key);
@@ -644,7 +648,7 @@ using namespace cast;
 // most of a CU), each split at least one first batch long, and
 // splits * k <= 64 for the combine wave.
 static int topk_splits(int32_t rows, int32_t vocab, int32_t dtype, int32_t k, int32_t want) {
-    const int per_batch = kTopkBatch * kTopkNT * (dtype == CAST_BF16 ? 8 : 4);
+    const int per_batch = kTopkBatch * kTopkNT * (dtype == CAST_FP32 ? 4 : 8);
     int cap = vocab / per_batch;
     cap = cap < 64 / k ? cap : 64 / k;
     cap = cap < kTopkMaxSplits ? cap : kTopkMaxSplits;
@@ -666,7 +670,7 @@ extern "C" int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t ro
                                size_t workspace_bytes, cast_stream_t stream) {
     if (rows < 0 || vocab <= 0 || logits_ld < vocab || k < 1 || k > kTopKMax || k > vocab || splits < 0)
         return CAST_ERR_SHAPE;
-    if (dtype != CAST_BF16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
+    if (dtype != CAST_BF16 && dtype != CAST_FP16 && dtype != CAST_FP32) return CAST_ERR_DTYPE;
     if (rows == 0) return CAST_OK;
     if (!logits || !top_idx || !top_lp) return CAST_ERR_NULL_POINTER;
     const int ns = topk_splits(rows, vocab, dtype, k, splits);
@@ -677,11 +681,17 @@ extern "C" int cast_draft_topk(const void *logits, int64_t logits_ld, int32_t ro
         if (reinterpret_cast<uintptr_t>(workspace) & 15) return CAST_ERR_ALIGNMENT;
         part = static_cast<TopkPart *>(workspace);
     }
-    const int epc = dtype == CAST_BF16 ? 8 : 4;
+    const int epc = dtype == CAST_FP32 ? 4 : 8;
     const int32_t per_e = (int32_t)(((int64_t)vocab + ns * epc - 1) / (ns * epc) * epc);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const dim3 grid(rows, ns);
-    if (dtype == CAST_BF16 && k <= 8)
+    if (dtype == CAST_FP16 && k <= 8)
+        draft_topk_kernel<true, 8, Fp16><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx,
+                                                                  top_lp);
+    else if (dtype == CAST_FP16)
+        draft_topk_kernel<true, kTopKMax, Fp16><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part,
+                                                                         top_idx, top_lp);
+    else if (dtype == CAST_BF16 && k <= 8)
         draft_topk_kernel<true, 8><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx, top_lp);
     else if (dtype == CAST_BF16)
         draft_topk_kernel<true, kTopKMax><<<grid, kTopkNT, 0, s>>>(logits, logits_ld, vocab, k, per_e, part, top_idx,

@@ -25,7 +25,8 @@ from .tree import MAX_PACK, TreeNode
 def topk_marginals(d_logits, k, *, on_device=False, splits=0):
     """Top-k token ids and log-probs at each future position.
 
-    d_logits: [L, V] (or [rows, V]) bf16/fp32 on the device.  Returns (indices
+    d_logits: [L, V] (or [rows, V]) bf16/fp16/fp32 on the device (other float
+    dtypes are widened to fp32 first).  Returns (indices
     int64 [L, k], values float32 [L, k]), moved to the host like the reference
     unless ``on_device``.  ``splits`` sets the workgroups per row (0: chosen
     from the shape); the results do not depend on it beyond float rounding
@@ -33,14 +34,14 @@ def topk_marginals(d_logits, k, *, on_device=False, splits=0):
     """
     lib = _lib.load()
     x = d_logits
-    if x.dtype not in (torch.bfloat16, torch.float32):
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
         x = x.float()
     if x.dim() != 2 or not x.is_cuda:
         raise ValueError("d_logits must be a [rows, V] device tensor")
     if x.stride(1) != 1:
         x = x.contiguous()
     rows, V = x.shape
-    dt = _lib.BF16 if x.dtype == torch.bfloat16 else _lib.FP32
+    dt = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16}.get(x.dtype, _lib.FP32)
     idx = torch.empty((rows, k), dtype=torch.int64, device=x.device)
     lp = torch.empty((rows, k), dtype=torch.float32, device=x.device)
     ws_bytes = lib.cast_draft_topk_workspace_size(rows, V, dt, k, int(splits)) if 1 <= k <= 16 else 0

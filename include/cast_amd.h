@@ -273,8 +273,7 @@ int cast_store_append(const void *const *k_pack, const void *const *v_pack, void
  * K5: drafter top-k marginals and best-first tree build on the device.
  * cast_draft_topk replaces topk_marginals (cast_trees/verify.py:8-12; the
  * log_softmax + topk + .cpu() of cast_trees/serving.py:126-128):
- *   logits   [rows, vocab] bf16 / fp32, row stride logits_ld elements
- *            (fp16 logits: widen to fp32 first)
+ *   logits   [rows, vocab] bf16 / fp16 / fp32, row stride logits_ld elements
  *   top_idx  int64 [rows][k] token ids, top_lp  float [rows][k] log-probs,
  *            ranked by descending log-probability, equal values in
  *            increasing index order (cast_trees/tree.py:20-26); 1 <= k <= 16,

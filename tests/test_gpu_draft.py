@@ -20,7 +20,8 @@ pytestmark = pytest.mark.gpu
 FIX = json.loads((Path(__file__).parent / "golden" / "tree_fixtures.json").read_text())
 
 
-@pytest.mark.parametrize("dtype,k", [(torch.float32, 8), (torch.bfloat16, 8), (torch.float32, 16)])
+@pytest.mark.parametrize("dtype,k", [(torch.float32, 8), (torch.bfloat16, 8), (torch.float32, 16), (torch.float16, 8),
+                                     (torch.float16, 16)])
 def test_topk_marginals_match_oracle(gpu, dtype, k):
     from cast_amd.draft import topk_marginals
     rng = np.random.default_rng(k)
@@ -42,7 +43,8 @@ def test_topk_marginals_match_oracle(gpu, dtype, k):
 
 
 @pytest.mark.parametrize("dtype,V,pad", [(torch.float32, 151936, 0), (torch.bfloat16, 151936, 0),
-                                         (torch.bfloat16, 1000, 3), (torch.float32, 50000, 1)])
+                                         (torch.bfloat16, 1000, 3), (torch.float32, 50000, 1),
+                                         (torch.float16, 151936, 0), (torch.float16, 1000, 3)])
 def test_topk_marginals_edge_rows(gpu, dtype, V, pad):
     # all-equal, increasing, decreasing, mostly -inf, integer-tied, NaN and +inf rows;
     # small vocabularies and unaligned row strides take the scalar path
