@@ -39,6 +39,27 @@ PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_MFMA_BF16 = 2.5e15    # FLOP/s, dense bf16
 PEAK_MFMA_FP32 = 157.3e12  # FLOP/s, dense fp32
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+BENCH_LIB = ROOT / "cast_amd" / "libcast_bench.so"
+_bench_lib = None
+
+
+def bench_lib():
+    """The measurement aids of cast_amd/csrc/bench/cast_bench.h (built by
+    cast_amd.build into libcast_bench.so beside the product library)."""
+    global _bench_lib
+    if _bench_lib is None:
+        import ctypes
+        import torch  # noqa: F401  (map torch's HIP runtime first)
+        if not BENCH_LIB.exists():
+            raise RuntimeError(f"{BENCH_LIB} is missing: build it with `python -m cast_amd.build`")
+        lib = ctypes.CDLL(str(BENCH_LIB))
+        P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+        lib.cast_clock_sample.argtypes = [P, I32, I32, P]
+        lib.cast_clock_sample.restype = ctypes.c_int
+        lib.cast_mfma_ceiling.argtypes = [P, I64, P, P, I32, I32, I32, P]
+        lib.cast_mfma_ceiling.restype = ctypes.c_int
+        _bench_lib = lib
+    return _bench_lib
 
 
 def log(*a):
@@ -557,7 +578,7 @@ class CeilingLoop:
     def __init__(self, dev):
         import torch
         from cast_amd import _lib
-        self.lib, self._lib = _lib.load(), _lib
+        self.lib, self._lib = bench_lib(), _lib
         g = torch.Generator(device=dev).manual_seed(5)
         self.src = torch.randn(1 << 20, generator=g, device=dev).to(torch.bfloat16)
         self.out = torch.empty(256 * 512, dtype=torch.float32, device=dev)
@@ -641,7 +662,7 @@ def clock_trace(dev, n, sets):
     time mean the clock moved, not the kernel."""
     import torch
     from cast_amd import _lib, scenarios
-    lib = _lib.load()
+    lib = bench_lib()
     wl = scenarios.qwen3_headline()
     h = Harness(wl, dev, sets=sets, kv_split=0)
     buf = torch.zeros(2 * n, dtype=torch.int64, device=dev)

@@ -18,6 +18,7 @@ ERR_PACK_TOO_LARGE = 3
 ERR_HIP = 10
 ERR_SCRATCH_LIMIT = 11
 ERR_DEVICE = 12
+ERR_ALIAS = 13
 
 FLAG_BAD_PACK = 1
 FLAG_BAD_OFFSETS = 2
@@ -52,8 +53,6 @@ SIGNATURES = {
     "cast_draft_topk": ([_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _SZ, _P], ctypes.c_int),
     "cast_draft_topk_workspace_size": ([_I32, _I32, _I32, _I32, _I32], _SZ),
     "cast_build_trees": ([_P, _P, _I32, _I32, _I32, _I32] + [_P] * 8, ctypes.c_int),
-    "cast_clock_sample": ([_P, _I32, _I32, _P], ctypes.c_int),
-    "cast_mfma_ceiling": ([_P, _I64, _P, _P, _I32, _I32, _I32, _P], ctypes.c_int),
     "cast_greedy_accept": ([_P, _I64, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _P, _P, _P, _P], ctypes.c_int),
 }
 

@@ -1,6 +1,12 @@
-"""Build libcast_amd.so for gfx950 from cast_amd/csrc/*.hip with hipcc.
+"""Build the HIP libraries for gfx950 with hipcc.
 
-    python -m cast_amd.build            # compile into cast_amd/libcast_amd.so
+    python -m cast_amd.build            # cast_amd/libcast_amd.so and libcast_bench.so
+
+libcast_amd.so (the product, the C ABI of include/cast_amd.h) comes from
+cast_amd/csrc/*.hip; libcast_bench.so (bench.py's measurement aids,
+cast_amd/csrc/bench/cast_bench.h) from cast_amd/csrc/bench/*.hip.  Compiler
+warnings are printed; a register-budget miss in an attention kernel
+(``-Wpass-failed``: an amdgpu_waves_per_eu target not met) fails the build.
 
 The library links against the HIP runtime with an rpath to torch's bundled
 ``torch/lib`` so that, with or without torch imported first, the process
@@ -19,6 +25,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libcast_amd.so"
+BENCH_OUT = PKG / "libcast_bench.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -53,34 +60,70 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    hipcc = _hipcc()
-    objdir = PKG / "_build"
-    objdir.mkdir(exist_ok=True)
-    inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
+def bench_sources():
+    return sorted((CSRC / "bench").glob("*.hip"))
 
-    def compile_one(src: Path) -> Path:
-        obj = objdir / (src.stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, *inc, "-c", str(src), "-o", str(obj)]
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
-        if verbose and res.stderr.strip():
-            print(res.stderr, file=sys.stderr)
-        return obj
 
-    with ThreadPoolExecutor(max_workers=4) as ex:
-        objs = list(ex.map(compile_one, sources()))
-    link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(OUT) + ".tmp"]
+# warnings that fail the build: a kernel that misses its occupancy target
+# runs with fewer waves than its tiling assumes
+_FATAL = ("failed to meet occupancy target",)
+
+
+def _compile(hipcc, src, objdir, inc):
+    obj = objdir / (src.stem + ".o")
+    cmd = [hipcc, *HIPCC_FLAGS, *inc, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
+    return obj, res.stderr
+
+
+def _link(hipcc, objs, out):
+    link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out) + ".tmp"]
     tl = _torch_lib()
     if tl is not None:
         link += [f"-Wl,-rpath,{tl}"]
     res = subprocess.run(link, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(str(OUT) + ".tmp", OUT)
+    os.replace(str(out) + ".tmp", out)
+
+
+def _warnings(stderr):
+    """hipcc's warnings, without its note that the host pass does not know
+    the device-only -packed-fp32-ops feature."""
+    keep = []
+    for line in stderr.splitlines():
+        if "packed-fp32-ops" in line and "not a recognized feature" in line:
+            continue
+        if line.strip():
+            keep.append(line)
+    return "\n".join(keep)
+
+
+def build(verbose: bool = True) -> Path:
+    hipcc = _hipcc()
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    (objdir / "bench").mkdir(exist_ok=True)
+    inc = ["-I", str(ROOT / "include"), "-I", str(CSRC), "-I", str(CSRC / "bench")]
+    jobs = [(s, objdir) for s in sources()] + [(s, objdir / "bench") for s in bench_sources()]
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        done = list(ex.map(lambda j: (j[0], *_compile(hipcc, j[0], j[1], inc)), jobs))
+    fatal = []
+    for src, _, err in done:
+        text = _warnings(err)
+        if text and verbose:
+            print(f"hipcc warnings in {src.name}:\n{text}", file=sys.stderr)
+        if any(f in text for f in _FATAL):
+            fatal.append(src.name)
+    if fatal:
+        raise RuntimeError(f"a kernel misses its occupancy target (amdgpu_waves_per_eu) in {', '.join(fatal)}")
+    n = len(sources())
+    _link(hipcc, [o for _, o, _ in done[:n]], OUT)
+    _link(hipcc, [o for _, o, _ in done[n:]], BENCH_OUT)
     return OUT
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build())

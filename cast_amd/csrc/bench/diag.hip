@@ -3,6 +3,7 @@
 // of clock frequency from a change of cycles per call; and an MFMA ceiling
 // loop at the attention kernel's launch shape, which measures what the
 // matrix pipes sustain on this part under that load.
+#include "cast_bench.h"
 #include "cast_common.hpp"
 
 namespace cast {

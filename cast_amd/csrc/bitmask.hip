@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kMaxPack) void tree_bitmask_kernel(
 
 using namespace cast;
 
-extern "C" int cast_abi_version(void) { return 3; }
+extern "C" int cast_abi_version(void) { return 4; }
 
 extern "C" const char *cast_status_string(int status) {
     switch (status) {
@@ -78,6 +78,7 @@ extern "C" const char *cast_status_string(int status) {
             return "the split-K scratch this call needs exceeds the no-allocation entry point's static array "
                    "(use a workspace, or a larger kv_split)";
         case CAST_ERR_DEVICE: return "the stream belongs to another device than the current one";
+        case CAST_ERR_ALIAS: return "an output overlaps an input that the kernels still read";
         default: return "unknown status";
     }
 }

@@ -8,7 +8,8 @@
 // layer (serving.py:62, [Hkv, total_q, D]) to store slots
 // store_len[b] .. store_len[b] + len(path) of buf[layer][b] ([B, Hkv, cap, D]).
 // The reference issues two advanced-indexing copies per layer; here one
-// workgroup per (request, layer, KV head) moves 16-byte chunks, driven by the
+// workgroup per (request, layer, KV head, column slice of at most 512 bytes
+// of each row) moves 16-byte chunks, driven by the
 // greedy-accept kernel's device-side path / path_len (no host round trip).
 // The per-layer base addresses come from host arrays and travel in the
 // kernel arguments, up to 64 layers per launch: a decode loop whose pack
@@ -18,8 +19,8 @@
 // then a barrier), so the copy is also correct in place: pack and store may
 // be the same tensor, as in the batch-one cache compaction of
 // cast_trees/verify.py:48-60 (gather_cache), where row n_prefix + keep[j]
-// moves to n_prefix + j.  Different (request, layer, head) triples never
-// share an address.
+// moves to n_prefix + j.  Different (request, layer, head, column slice)
+// tuples never share an address.
 #include "cast_common.hpp"
 
 namespace cast {
@@ -34,6 +35,7 @@ struct AppendArgs {
     void *k_store[kAppendLayersPerLaunch];        // store K of each layer
     void *v_store[kAppendLayersPerLaunch];
     int32_t batch, total_q, cap, Hkv, chunks;     // chunks = 16-byte pieces per (row, head)
+    int32_t slices;                               // column slices per (row, head): ceil(chunks / 32)
     int32_t first_launch;                         // writes new_len and the per-request flag
     const int32_t *src_row;      // [batch] packed row of request b's root (cu_q of its pack)
     const int32_t *path;         // [batch][path_stride] accepted node indices (-1 padded)
@@ -47,25 +49,30 @@ struct AppendArgs {
 };
 
 constexpr int kAppendThreads = 256;
-constexpr int kAppendMaxChunks = 32;   // 16-byte chunks per (row, head): head_dim * esz <= 512 B
+constexpr int kAppendMaxChunks = 32;   // 16-byte chunks of each row one workgroup moves (512 B)
 constexpr int kAppendPerThread = kMaxPack * kAppendMaxChunks / kAppendThreads;
 
 __global__ __launch_bounds__(kAppendThreads) void store_append_kernel(AppendArgs a) {
-    const int b = blockIdx.x, layer = blockIdx.y, h = blockIdx.z;
+    const int b = blockIdx.x, layer = blockIdx.y;
+    const int h = blockIdx.z / a.slices, slice = blockIdx.z % a.slices;
+    // this workgroup's columns of every row: chunks [c0, c0 + width)
+    const int c0 = slice * kAppendMaxChunks;
+    const int width = min(kAppendMaxChunks, a.chunks - c0);
     const int n = a.path_len[b];
     const int s0 = a.store_len[b];
     const int root = a.src_row[b];
     const int count = n + 1;     // root + accepted nodes
     if (n < 0 || n >= kMaxPack || s0 < 0 || s0 + count > a.cap || root < 0 || root >= a.total_q) {
-        if (threadIdx.x == 0 && layer == 0 && h == 0 && a.first_launch) raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
+        if (threadIdx.x == 0 && layer == 0 && blockIdx.z == 0 && a.first_launch)
+            raise_flag(a.status, CAST_FLAG_BAD_OFFSETS);
         return;
     }
-    if (threadIdx.x == 0 && layer == 0 && h == 0 && a.first_launch && a.new_len) a.new_len[b] = s0 + count;
+    if (threadIdx.x == 0 && layer == 0 && blockIdx.z == 0 && a.first_launch && a.new_len) a.new_len[b] = s0 + count;
     const char *kp = static_cast<const char *>(a.k_pack[layer]) + (int64_t)h * a.kp_head;
     const char *vp = static_cast<const char *>(a.v_pack[layer]) + (int64_t)h * a.vp_head;
     char *ks = static_cast<char *>(a.k_store[layer]) + (int64_t)b * a.ks_batch + (int64_t)h * a.ks_head;
     char *vs = static_cast<char *>(a.v_store[layer]) + (int64_t)b * a.vs_batch + (int64_t)h * a.vs_head;
-    const int total = count * a.chunks;   // <= kMaxPack * kAppendMaxChunks
+    const int total = count * width;   // <= kMaxPack * kAppendMaxChunks
     // phase 1: every row this workgroup moves, into registers
     u32x4 kx[kAppendPerThread], vx[kAppendPerThread];
     bool ok[kAppendPerThread];
@@ -74,7 +81,7 @@ __global__ __launch_bounds__(kAppendThreads) void store_append_kernel(AppendArgs
         const int idx = threadIdx.x + u * kAppendThreads;
         ok[u] = false;
         if (idx < total) {
-            const int j = idx / a.chunks, c = idx % a.chunks;
+            const int j = idx / width, c = c0 + idx % width;
             // keep[j]: the root (pack index 0), then node path[j-1] at pack index path[j-1] + 1
             int pk = 0;
             if (j > 0) pk = a.path[(int64_t)b * a.path_stride + j - 1] + 1;
@@ -95,7 +102,7 @@ __global__ __launch_bounds__(kAppendThreads) void store_append_kernel(AppendArgs
     for (int u = 0; u < kAppendPerThread; ++u) {
         const int idx = threadIdx.x + u * kAppendThreads;
         if (idx < total && ok[u]) {
-            const int j = idx / a.chunks, c = idx % a.chunks;
+            const int j = idx / width, c = c0 + idx % width;
             const int64_t dst = (int64_t)(s0 + j);
             *reinterpret_cast<u32x4 *>(ks + dst * a.ks_tok + c * 16) = kx[u];
             *reinterpret_cast<u32x4 *>(vs + dst * a.vs_tok + c * 16) = vx[u];
@@ -123,7 +130,21 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     if (!k_pack || !v_pack || !k_store || !v_store || !src_row || !path || !path_len || !store_len)
         return CAST_ERR_NULL_POINTER;
     const int64_t esz = dtype == CAST_FP32 ? 4 : 2;   // a row copy: only the element size matters
-    if ((head_dim * esz) % 16 || head_dim * esz > 16 * kAppendMaxChunks) return CAST_ERR_HEAD_DIM;
+    if ((head_dim * esz) % 16 || head_dim * esz > 16 * 1024) return CAST_ERR_HEAD_DIM;
+    const int64_t slices = (head_dim * esz / 16 + kAppendMaxChunks - 1) / kAppendMaxChunks;
+    if ((int64_t)num_kv_heads * slices > 65535) return CAST_ERR_SHAPE;
+    // new_len is written while other workgroups (and later launches) still
+    // read store_len, path_len, src_row and path: it must not overlap them
+    if (new_len) {
+        auto overlaps = [&](const int32_t *p, int64_t n) {
+            const uintptr_t a0 = reinterpret_cast<uintptr_t>(new_len), a1 = a0 + (uintptr_t)batch * 4;
+            const uintptr_t b0 = reinterpret_cast<uintptr_t>(p), b1 = b0 + (uintptr_t)n * 4;
+            return a0 < b1 && b0 < a1;
+        };
+        if (overlaps(store_len, batch) || overlaps(path_len, batch) || overlaps(src_row, batch) ||
+            overlaps(path, (int64_t)batch * path_stride))
+            return CAST_ERR_ALIAS;
+    }
     const int64_t strides[10] = {kp_tok, kp_head, vp_tok, vp_head, ks_batch, ks_head, ks_tok, vs_batch, vs_head, vs_tok};
     for (int64_t s : strides)
         if ((s * esz) % 16) return CAST_ERR_ALIGNMENT;
@@ -135,6 +156,7 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
     a.cap = cap;
     a.Hkv = num_kv_heads;
     a.chunks = (int32_t)(head_dim * esz / 16);
+    a.slices = (a.chunks + kAppendMaxChunks - 1) / kAppendMaxChunks;
     a.src_row = src_row;
     a.path = path;
     a.path_stride = path_stride;
@@ -161,7 +183,7 @@ extern "C" int cast_store_append(const void *const *k_pack, const void *const *v
             a.v_store[l] = v_store[l0 + l];
         }
         a.first_launch = l0 == 0;
-        store_append_kernel<<<dim3(batch, n, num_kv_heads), kAppendThreads, 0,
+        store_append_kernel<<<dim3(batch, n, num_kv_heads * a.slices), kAppendThreads, 0,
                               reinterpret_cast<hipStream_t>(stream)>>>(a);
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     }

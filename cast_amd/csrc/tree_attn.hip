@@ -38,7 +38,6 @@
 
 namespace cast {
 
-constexpr int kNumCU = 256;              // MI355X compute units
 constexpr int kNoSplit = 1 << 30;        // chunk value meaning "one split"
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -83,6 +82,7 @@ struct AttnArgs {
     float scale_log2;   // sm_scale * log2(e)
     int32_t chunk;      // keys per split, multiple of 64 (kNoSplit = no split)
     int32_t max_rows;   // longest key source (rows) the MFMA kernel can address
+    int32_t xcds;       // XCDs of the device: workgroup x runs on XCD x % xcds
     int32_t rows_wg;    // query rows per workgroup
     int32_t comb_groups;  // combine kernel: head groups per packed token
     float *part_o;      // [part_rows][Hq][D] fp32, normalised partial outputs
@@ -296,23 +296,23 @@ __device__ bool find_request(const AttnArgs &a, int64_t w, bool by_token, Seq &s
 // ---- longest-first schedule (batches of up to 64 requests).  Work is
 // grouped per (request, KV head, key split); a group's rb row blocks read
 // the same keys.  Groups are ranked by keys per group (split_len) in
-// descending order and dealt to the 8 XCDs round-robin (workgroup x runs on
-// XCD x % 8), each group's row blocks taking consecutive slots of one XCD so
+// descending order and dealt to the nx XCDs round-robin (workgroup x runs on
+// XCD x % nx), each group's row blocks taking consecutive slots of one XCD so
 // that they share its L2.  Within an XCD workgroups start in slot order, so
 // each XCD works through its groups longest first (a greedy longest-
 // processing-time schedule): short groups fill in behind long ones instead
 // of trailing alone.  Every group has R = the batch's largest rb slots;
 // slots past a request's own rb exit at once.
 
-// Slot count of the longest-first grid: every XCD holds at most
-// ceil(groups / 8) groups of at most rbmax row blocks each.
-__host__ __device__ __forceinline__ int64_t sorted_slots(int64_t groups, int64_t rbmax) {
-    return ((groups + 7) / 8) * 8 * rbmax;
+// Slot count of the longest-first grid: every one of the nx XCDs holds at
+// most ceil(groups / nx) groups of at most rbmax row blocks each.
+__host__ __device__ __forceinline__ int64_t sorted_slots(int64_t groups, int64_t rbmax, int nx) {
+    return ((groups + nx - 1) / nx) * nx * rbmax;
 }
 
 // The (request, KV head, split, row block) of slot x, or false for an empty
 // slot.  Requires batch <= 64: lane j holds request j (t, and loaded when it
-// passed load_seq).  XCD x % 8 takes every 8th group of the longest-first
+// passed load_seq).  XCD x % nx takes every nx-th group of the longest-first
 // order, and its slots are those groups' row blocks, packed densely in that
 // order.  Wave-uniform result.
 __device__ bool locate_sorted(const AttnArgs &a, int64_t x, const Seq &t, bool loaded, Seq &s, int &h, int &split,
@@ -332,11 +332,12 @@ __device__ bool locate_sorted(const AttnArgs &a, int64_t x, const Seq &t, bool l
         const int nj = __builtin_amdgcn_readlane(ng, j);
         off += kj < key ? nj : 0;
     }
-    // its groups dealt to this XCD (g in [off, off + ng), g % 8 == xcd), and
+    // its groups dealt to this XCD (g in [off, off + ng), g % nx == xcd), and
     // the slots they take there
-    const int xcd = (int)(x & 7);
-    const int k = (int)(x >> 3);
-    auto on_xcd = [xcd](int n) { return (n + 7 - xcd) >> 3; };   // #g in [0, n) with g % 8 == xcd
+    const int nx = a.xcds;
+    const int xcd = (int)(x % nx);
+    const int k = (int)(x / nx);
+    auto on_xcd = [xcd, nx](int n) { return (n + nx - 1 - xcd) / nx; };   // #g in [0, n) with g % nx == xcd
     const int slots = ok ? (on_xcd(off + ng) - on_xcd(off)) * t.rb : 0;
     int start = 0;
     for (int j = 0; j < a.batch; ++j) {
@@ -351,7 +352,7 @@ __device__ bool locate_sorted(const AttnArgs &a, int64_t x, const Seq &t, bool l
     s.part_off = bcast(p_excl, b);
     const int kk = k - bcast(start, b);
     const int off_b = bcast(off, b);
-    const int g = off_b + ((xcd - off_b) & 7) + 8 * (kk / s.rb);   // the (kk / rb)-th of its groups here
+    const int g = off_b + ((xcd - off_b) % nx + nx) % nx + nx * (kk / s.rb);   // the (kk / rb)-th of its groups here
     const int local = g - off_b;
     h = local / s.ns;
     split = local % s.ns;
@@ -443,7 +444,7 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 // the workgroup has none (or the batch was rejected).  Batches of up to 64
 // requests use the longest-first schedule; larger ones take items in batch
 // order, consecutive items (the row blocks of one key split) on one XCD
-// (workgroups are dealt to the 8 XCDs round-robin) so that they share its L2.
+// (workgroups are dealt to the XCDs round-robin) so that they share its L2.
 __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, int &split, int &rb) {
     if (a.batch <= 64) {
         // one round of metadata loads serves the totals and the schedule
@@ -458,10 +459,11 @@ __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, 
     const BatchTotals tot = batch_totals(a);
     if (!batch_prologue(a, tot)) return false;
     const int64_t total = tot.items;
-    const int64_t n8 = (total + 7) & ~(int64_t)7;
+    const int nx = a.xcds;
+    const int64_t n8 = (total + nx - 1) / nx * nx;
     const int64_t x = blockIdx.x;
     if (x >= n8) return false;
-    const int64_t w = (x & 7) * (n8 >> 3) + (x >> 3);
+    const int64_t w = (x % nx) * (n8 / nx) + x / nx;
     if (w >= total) return false;
     int local;
     if (!find_request(a, w, false, sq, local)) return false;
@@ -474,7 +476,10 @@ __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, 
 // WPE: waves per SIMD the register budget is sized for.  2 (256 registers a
 // lane) for head_dim 64 and 128; 1 (512) for head_dim 256, whose O^T
 // accumulators (128 registers), Q^T operand (64), scores and staged K/V
-// tiles take about 330.
+// tiles take about 330, and for the 2-wave head_dim-128 instance, whose 128
+// threads each stage four times the 8-wave instance's share of a K tile
+// (about 330 registers): its 72 KB of LDS allow two such workgroups per
+// CU, one wave per SIMD, either way.
 template <int D, int WAVES, bool STORE, typename E, int WPE = 2>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void tree_attn_mfma_kernel(AttnArgs a) {
@@ -553,8 +558,8 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     const int pk_begin = max(k_begin, sq.S);
     const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
     const int ntiles = n_pre + n_pack;
-    auto tile_t0 = [&](int t) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
-    auto tile_valid = [&](int t) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
+    auto tile_t0 = [&](int t) __attribute__((always_inline)) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
+    auto tile_valid = [&](int t) __attribute__((always_inline)) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
 
     // ---- global -> register staging of one tile.  Each key source of this
     // (request, head) is one buffer resource that ends at its last row (the
@@ -565,20 +570,14 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     const uint32_t ksb_pre = (uint32_t)kv.kpre_t * 2u, vsb_pre = (uint32_t)kv.vpre_t * 2u;
     const uint32_t ksb_pack = (uint32_t)kv.kpack_t * 2u, vsb_pack = (uint32_t)kv.vpack_t * 2u;
     const int rows_pre = STORE ? sq.S : sq.T;
-    const __amdgpu_buffer_rsrc_t kr_pre = seg_rsrc(kv.kpre, rows_pre, ksb_pre, D * 2);
-    const __amdgpu_buffer_rsrc_t vr_pre = seg_rsrc(kv.vpre, rows_pre, vsb_pre, D * 2);
-    const __amdgpu_buffer_rsrc_t kr_pack = seg_rsrc(kv.kpack, STORE ? sq.P : 0, ksb_pack, D * 2);
-    const __amdgpu_buffer_rsrc_t vr_pack = seg_rsrc(kv.vpack, STORE ? sq.P : 0, vsb_pack, D * 2);
     u32x4 kst[K_PER_T];
     u32x4 vst[V_PER_T][8];
-    auto fetch = [&](int t) {
-        const bool pre = !STORE || t < n_pre;
-        const int t0 = tile_t0(t);
-        const uint32_t row0 = (uint32_t)(pre ? t0 : t0 - sq.S);   // first row within its source
-        const __amdgpu_buffer_rsrc_t krs = pre ? kr_pre : kr_pack;
-        const __amdgpu_buffer_rsrc_t vrs = pre ? vr_pre : vr_pack;
-        const uint32_t ksb = pre ? ksb_pre : ksb_pack;
-        const uint32_t vsb = pre ? vsb_pre : vsb_pack;
+    // loads of one tile from one source (base, rows, byte strides); row0 is
+    // the tile's first row within that source
+    auto fetch_from = [&](const uint16_t *kb, const uint16_t *vb, int rows, uint32_t ksb, uint32_t vsb,
+                          uint32_t row0) __attribute__((always_inline)) {
+        const __amdgpu_buffer_rsrc_t krs = seg_rsrc(kb, rows, ksb, D * 2);
+        const __amdgpu_buffer_rsrc_t vrs = seg_rsrc(vb, rows, vsb, D * 2);
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
             const int cidx = tid + it * NT;
@@ -598,8 +597,18 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                 vst[it][i] = load16(vrs, __umul24(v0 + 8 * (i >> 2) + (i & 3), vsb) + dch * 16);
         }
     };
+    // the source is chosen by a (wave-uniform) branch, not by selecting
+    // between the two sources' values, which the compiler may lower to
+    // loads through a private array
+    auto fetch = [&](int t) __attribute__((always_inline)) {
+        const int t0 = tile_t0(t);
+        if (!STORE || t < n_pre)
+            fetch_from(kv.kpre, kv.vpre, rows_pre, ksb_pre, vsb_pre, (uint32_t)t0);
+        else
+            fetch_from(kv.kpack, kv.vpack, sq.P, ksb_pack, vsb_pack, (uint32_t)(t0 - sq.S));
+    };
     // ---- register -> LDS: K as is; V as 8x8 transposed blocks
-    auto publish = [&](int buf) {
+    auto publish = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
             const int cidx = tid + it * NT;
@@ -819,8 +828,12 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 // output blocks.  The product is MFMA-bound (16 x the bf16 cycles per
 // flop): staging and softmax are small beside it.
 // --------------------------------------------------------------------------
-template <int D, int WAVES, bool STORE>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2)))
+// WPE: waves per SIMD the register budget is sized for: 2, except the
+// 4-wave head_dim-128 instance (1): its threads each stage twice the 8-wave
+// instance's share of a tile, and its 135 KB of LDS leave room for one
+// workgroup (one wave per SIMD) per CU anyway.
+template <int D, int WAVES, bool STORE, int WPE = 2>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void tree_attn_f32_kernel(AttnArgs a) {
     constexpr int NT = WAVES * 64;
     constexpr int BN = 64;                 // keys per tile
@@ -887,8 +900,8 @@ void tree_attn_f32_kernel(AttnArgs a) {
     const int pk_begin = max(k_begin, sq.S);
     const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
     const int ntiles = n_pre + n_pack;
-    auto tile_t0 = [&](int t) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
-    auto tile_valid = [&](int t) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
+    auto tile_t0 = [&](int t) __attribute__((always_inline)) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
+    auto tile_valid = [&](int t) __attribute__((always_inline)) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
 
     const uint32_t ksb_pre = (uint32_t)kv.kpre_t * 4u, vsb_pre = (uint32_t)kv.vpre_t * 4u;
     const uint32_t ksb_pack = (uint32_t)kv.kpack_t * 4u, vsb_pack = (uint32_t)kv.vpack_t * 4u;
@@ -899,7 +912,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t vr_pack = seg_rsrc(kv.vpack, STORE ? sq.P : 0, vsb_pack, D * 4);
     u32x4 kst[K_PER_T];
     u32x4 vst[V_PER_T][DB];
-    auto fetch = [&](int t) {
+    auto fetch = [&](int t) __attribute__((always_inline)) {
         const bool pre = !STORE || t < n_pre;
         const int t0 = tile_t0(t);
         const uint32_t row0 = (uint32_t)(pre ? t0 : t0 - sq.S);
@@ -925,7 +938,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
         }
     };
     // register -> LDS: K as is; V with d = 32*db + l stored at l*DB + db
-    auto publish = [&](int buf) {
+    auto publish = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
             const int cidx = tid + it * NT;
@@ -1348,6 +1361,32 @@ __global__ __launch_bounds__(256) void tree_attn_generic_kernel(AttnArgs a, int 
 // --------------------------------------------------------------------------
 // Host side
 // --------------------------------------------------------------------------
+// The current device's compute units and XCDs, looked up once per device;
+// an MI355X's 256 and 8 where no device is visible (host-only size queries
+// on a machine without a GPU).
+struct Topology {
+    int cus, xcds;
+};
+constexpr int kMaxTopoDevices = 64;
+static Topology device_topology() {
+    static std::mutex mu;
+    static Topology cache[kMaxTopoDevices];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxTopoDevices) return {256, 8};
+    std::lock_guard<std::mutex> lock(mu);
+    Topology &t = cache[dev];
+    if (t.cus == 0) {
+        int cus = 0, xcds = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || xcds <= 0 ||
+            cus % xcds)
+            xcds = 1;
+        t = {cus, xcds};
+    }
+    return t;
+}
+
 static bool mfma_path(int32_t dtype, int32_t D) {
     if (dtype == CAST_FP32) return D == 64 || D == 128;
     return (dtype == CAST_BF16 || dtype == CAST_FP16) && (D == 64 || D == 128 || D == 256);
@@ -1377,8 +1416,9 @@ static int32_t resolve_chunk(int32_t batch, int32_t total_q, int32_t total_kv, i
     const int64_t rb = (p_est * G + rows_wg - 1) / rows_wg;
     const int64_t units = (int64_t)Hkv * batch * (rb > 0 ? rb : 1);
     const int64_t t_avg = (total_kv + batch - 1) / batch;
-    if (units >= kNumCU) return kNoSplit;
-    int64_t chunk = (t_avg * units + kNumCU - 1) / kNumCU;
+    const int cus = device_topology().cus;
+    if (units >= cus) return kNoSplit;
+    int64_t chunk = (t_avg * units + cus - 1) / cus;
     chunk = ((chunk + 63) / 64) * 64;
     if (chunk < kMinChunk) chunk = kMinChunk;
     if (chunk >= t_avg) return kNoSplit;
@@ -1528,39 +1568,41 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     const int64_t rbmax = (pmax * a.G + a.rows_wg - 1) / a.rows_wg;
     const int64_t nsplit = a.chunk == kNoSplit ? batch : ((int64_t)total_kv + a.chunk - 1) / a.chunk + batch;
     int64_t items = (int64_t)num_kv_heads * rbmax * nsplit;
-    items = batch <= 64 ? sorted_slots((int64_t)num_kv_heads * nsplit, rbmax) : (items + 7) & ~(int64_t)7;
+    a.xcds = device_topology().xcds;
+    items = batch <= 64 ? sorted_slots((int64_t)num_kv_heads * nsplit, rbmax, a.xcds)
+                        : (items + a.xcds - 1) / a.xcds * a.xcds;
     const unsigned grid = (unsigned)items;
-#define CAST_LAUNCH_E(DD, W, E)                                                \
-    (kv.store ? tree_attn_mfma_kernel<DD, W, true, E><<<grid, W * 64, 0, st>>>(a) \
-              : tree_attn_mfma_kernel<DD, W, false, E><<<grid, W * 64, 0, st>>>(a))
-#define CAST_LAUNCH(DD, W) (f16 ? CAST_LAUNCH_E(DD, W, Fp16) : CAST_LAUNCH_E(DD, W, Bf16))
+#define CAST_LAUNCH_E(DD, W, E, WPE)                                                \
+    (kv.store ? tree_attn_mfma_kernel<DD, W, true, E, WPE><<<grid, W * 64, 0, st>>>(a) \
+              : tree_attn_mfma_kernel<DD, W, false, E, WPE><<<grid, W * 64, 0, st>>>(a))
+#define CAST_LAUNCH(DD, W, WPE) (f16 ? CAST_LAUNCH_E(DD, W, Fp16, WPE) : CAST_LAUNCH_E(DD, W, Bf16, WPE))
 #define CAST_LAUNCH_WIDE_E(W, E)                                                       \
     (kv.store ? tree_attn_mfma_kernel<256, W, true, E, 1><<<grid, W * 64, 0, st>>>(a) \
               : tree_attn_mfma_kernel<256, W, false, E, 1><<<grid, W * 64, 0, st>>>(a))
 #define CAST_LAUNCH_WIDE(W) (f16 ? CAST_LAUNCH_WIDE_E(W, Fp16) : CAST_LAUNCH_WIDE_E(W, Bf16))
-#define CAST_LAUNCH_F32(DD, W)                                                \
-    (kv.store ? tree_attn_f32_kernel<DD, W, true><<<grid, W * 64, 0, st>>>(a) \
-              : tree_attn_f32_kernel<DD, W, false><<<grid, W * 64, 0, st>>>(a))
+#define CAST_LAUNCH_F32(DD, W, WPE)                                                \
+    (kv.store ? tree_attn_f32_kernel<DD, W, true, WPE><<<grid, W * 64, 0, st>>>(a) \
+              : tree_attn_f32_kernel<DD, W, false, WPE><<<grid, W * 64, 0, st>>>(a))
     const bool f16 = dtype == CAST_FP16;
     if (!(stages & kStageAttn)) {
     } else if (dtype == CAST_FP32) {
         if (head_dim == 128) {
-            if (waves == 4) CAST_LAUNCH_F32(128, 4);
-            else CAST_LAUNCH_F32(128, 8);
+            if (waves == 4) CAST_LAUNCH_F32(128, 4, 1);
+            else CAST_LAUNCH_F32(128, 8, 2);
         } else {
-            if (waves == 4) CAST_LAUNCH_F32(64, 4);
-            else CAST_LAUNCH_F32(64, 8);
+            if (waves == 4) CAST_LAUNCH_F32(64, 4, 2);
+            else CAST_LAUNCH_F32(64, 8, 2);
         }
     } else if (head_dim == 256) {
         CAST_LAUNCH_WIDE(4);
     } else if (head_dim == 128) {
-        if (waves == 2) CAST_LAUNCH(128, 2);
-        else if (waves == 4) CAST_LAUNCH(128, 4);
-        else CAST_LAUNCH(128, 8);
+        if (waves == 2) CAST_LAUNCH(128, 2, 1);
+        else if (waves == 4) CAST_LAUNCH(128, 4, 2);
+        else CAST_LAUNCH(128, 8, 2);
     } else {
-        if (waves == 2) CAST_LAUNCH(64, 2);
-        else if (waves == 4) CAST_LAUNCH(64, 4);
-        else CAST_LAUNCH(64, 8);
+        if (waves == 2) CAST_LAUNCH(64, 2, 2);
+        else if (waves == 4) CAST_LAUNCH(64, 4, 2);
+        else CAST_LAUNCH(64, 8, 2);
     }
 #undef CAST_LAUNCH
 #undef CAST_LAUNCH_E

@@ -221,6 +221,39 @@ def random_parent_batch(seed=0, B=8, Hq=32, Hkv=8, D=128, s_lo=200, s_hi=400, p_
                  qkv_scale)
 
 
+def reference_test_batch(seed=0, B=8, Hq=32, Hkv=8, D=128):
+    """The exact inputs of the reference's own kernel test
+    (cast_trees tests/test_tree_attn.py:11-37): one CPU ``torch.Generator``
+    seeded with ``seed`` draws, request by request, S ~ U[200, 400),
+    P ~ U[2, 64), the parents ``parent[i] ~ U[0, i)`` one at a time, then
+    q [P, Hq, D], k [S+P, Hkv, D] and v [S+P, Hkv, D] from N(0, 1), in that
+    order.  Returns (workload, q, k, v) with fp32 tensors on the CPU; the
+    workload holds the same trees and prefixes (its own ``qkv`` draws other
+    tensors).
+    """
+    import torch
+    from .tree import TreeNode
+    g = torch.Generator().manual_seed(seed)
+    draw_int = lambda lo, hi: int(torch.randint(lo, hi, (1,), generator=g))
+    trees, prefix, qs, ks, vs = [], [], [], [], []
+    for _ in range(B):
+        S = draw_int(200, 400)
+        P = draw_int(2, 64)
+        par = [-1] + [draw_int(0, i) for i in range(1, P)]
+        qs.append(torch.randn(P, Hq, D, generator=g))
+        ks.append(torch.randn(S + P, Hkv, D, generator=g))
+        vs.append(torch.randn(S + P, Hkv, D, generator=g))
+        depth = [0] * P
+        nodes = []
+        for i in range(1, P):
+            depth[i] = depth[par[i]] + 1
+            nodes.append(TreeNode(0, depth[i], par[i] - 1, 0.0))
+        trees.append(nodes)
+        prefix.append(S)
+    wl = _make("reference-kernel-test", trees, prefix, dict(Hq=Hq, Hkv=Hkv, D=D, vocab=1), "fp32", seed, 1.0)
+    return wl, torch.cat(qs), torch.cat(ks), torch.cat(vs)
+
+
 CONFIGS = {
     "cpu-plumbing": cpu_plumbing,
     "qwen3-8b-single": qwen3_single,

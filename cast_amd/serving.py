@@ -411,8 +411,14 @@ _TREE_META = {"ref": None, "key": None, "meta": None}
 def _tree_meta(mask, n_kv):
     """Kernel metadata for a (1, 1, n, S + n) additive tree mask, or None when
     the mask is not one (a masked prefix key, or a pack longer than 128).  The
-    same mask object is handed to every layer of one forward: derived once."""
+    same mask object is handed to every layer of one forward: derived once.
+    A mask made by ``cast_amd.verify.tree_attention_mask`` carries its
+    metadata (built on the host from the same ancestor matrix) and is never
+    read back; any other mask is checked on the device, with one host wait."""
     key = (None if mask.is_inference() else mask._version, n_kv)
+    tag = getattr(mask, "_cast_tree_meta", None)
+    if tag is not None and (tag[0], tag[1]) == key:
+        return tag[2]
     ref = _TREE_META["ref"]
     if ref is not None and ref() is mask and _TREE_META["key"] == key:
         return _TREE_META["meta"]

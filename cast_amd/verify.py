@@ -141,14 +141,50 @@ def walk_tree(nodes, logits, temperature=0.0, d_logits=None, draft_temp=1.0, gen
     return walk_trees([nodes], logits[:1 + len(nodes)])[0]
 
 
+def ancestor_words(vis):
+    """Two 64-bit words per row of a boolean visibility matrix (n <= 128):
+    bit j of word j // 64 is vis[i, j] (the layout of the reference's int64
+    mask, cast_trees/serving.py:218-222, extended to a second word)."""
+    vis = np.asarray(vis, dtype=bool)
+    n = vis.shape[0]
+    if vis.shape != (n, n) or n > MAX_PACK:
+        raise ValueError(f"a square visibility matrix of at most {MAX_PACK} rows")
+    bits = np.zeros((n, 2 * 64), dtype=np.uint8)
+    bits[:, :n] = vis
+    return np.packbits(bits, axis=1, bitorder="little").view(np.int64)
+
+
 def tree_attention_mask(n_prefix, nodes, device, dtype):
     """Additive mask (1, 1, 1+N, n_prefix+1+N): 0 where visible (the prefix
-    and each row's ancestor chain), ``finfo(dtype).min`` elsewhere."""
-    vis = torch.from_numpy(ancestor_matrix(nodes))
+    and each row's ancestor chain), ``finfo(dtype).min`` elsewhere.
+
+    On a GPU the mask is uploaded from pinned memory without a host wait,
+    and the kernel metadata of the "cast_tree" attention (cu_q, cu_kv,
+    prefix_len, pack_len and the ancestor words, from the same host
+    ancestor matrix) rides along as an attribute of the returned tensor, so
+    the verify forward reads nothing back from the device.
+    """
+    vis_np = ancestor_matrix(nodes)
+    vis = torch.from_numpy(vis_np)
     n = vis.shape[0]
-    mask = torch.zeros((1, 1, n, n_prefix + n), dtype=dtype)
+    device = torch.device(device)
+    pinned = device.type == "cuda"
+    mask = torch.zeros((1, 1, n, n_prefix + n), dtype=dtype, pin_memory=pinned)
     mask[0, 0, :, n_prefix:].masked_fill_(~vis, torch.finfo(dtype).min)
-    return mask.to(device)
+    if not pinned:
+        return mask.to(device)
+    dev_mask = mask.to(device, non_blocking=True)
+    if n <= MAX_PACK:
+        # int32 [4n + 6]: the words (n x 2 int64) first, then
+        # cu_q [0, n], cu_kv [0, S + n], prefix_len [S], pack_len [n]
+        host = torch.zeros(4 * n + 6, dtype=torch.int32, pin_memory=True)
+        host[:4 * n].view(torch.int64).view(n, 2).copy_(torch.from_numpy(ancestor_words(vis_np)))
+        host[4 * n:] = torch.tensor([0, n, 0, n_prefix + n, n_prefix, n], dtype=torch.int32)
+        d = host.to(device, non_blocking=True)
+        meta = (d[4 * n:4 * n + 2], d[4 * n + 2:4 * n + 4], d[4 * n + 4:4 * n + 5], d[4 * n + 5:],
+                d[:4 * n].view(torch.int64).view(n, 2))
+        dev_mask._cast_tree_meta = (None if dev_mask.is_inference() else dev_mask._version, n_prefix + n, meta)
+    return dev_mask
 
 
 def cache_layers(cache):

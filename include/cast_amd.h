@@ -42,7 +42,8 @@ enum cast_status {
     CAST_ERR_HIP = 10,             /* a HIP runtime call or launch failed */
     CAST_ERR_SCRATCH_LIMIT = 11,   /* the no-allocation entry point would need more
                                       split-K scratch than its static array holds */
-    CAST_ERR_DEVICE = 12           /* the stream's device is not the current device */
+    CAST_ERR_DEVICE = 12,          /* the stream's device is not the current device */
+    CAST_ERR_ALIAS = 13            /* an output overlaps an input the kernels still read */
 };
 
 /* Bits a kernel ORs into the optional device status word (int32). */
@@ -250,11 +251,16 @@ int cast_greedy_accept(const void *logits, int64_t logits_ld, int32_t vocab, int
  *   path      int32 [batch][path_stride >= 128]  accepted node indices, as
  *             written by cast_greedy_accept;  path_len int32 [batch]
  *   store_len int32 [batch]  tokens already in request b's slot
- *   new_len   int32 [batch]  out (nullable): store_len + path_len + 1
+ *   new_len   int32 [batch]  out (nullable): store_len + path_len + 1.  It
+ *             must not overlap store_len, path_len, src_row or path (other
+ *             workgroups still read them when it is written): an in-place
+ *             length update is refused with CAST_ERR_ALIAS
  * Request b keeps its root and its accepted nodes (keep = [0] + [i + 1 for
  * i in path], cast_trees/serving.py:328-330) at slots store_len[b] .. in
  * order.  A request that would pass `cap` is skipped and flagged
- * CAST_FLAG_BAD_OFFSETS.  head_dim * element size <= 512 bytes.
+ * CAST_FLAG_BAD_OFFSETS.  head_dim * element size: a multiple of 16 bytes,
+ * at most 16 KiB (rows above 512 bytes are moved in 512-byte column slices,
+ * one workgroup each).
  * Pack and store may be the same memory (each (request, layer, head) is
  * read whole before it is written): this is also the batch-one in-place
  * compaction of cast_trees/verify.py:48-60 (gather_cache), with the pack
@@ -312,32 +318,6 @@ int cast_build_trees(const int64_t *top_idx, const void *top_lp, int32_t lp_dtyp
                      int32_t *parent, double *score, int32_t *n_nodes, int32_t *status,
                      cast_stream_t stream);
 
-/* ---------------------------------------------------------------------
- * Measurement aid, no counterpart in the reference.  Samples the shader
- * clock: writes out[2*slot] = shader cycles and out[2*slot + 1] = ticks of
- * the constant 100 MHz counter over a fixed chain of `iters` dependent FMAs
- * (one workgroup, stream-ordered).  cycles / ticks * 100 MHz is the shader
- * clock at that point of the stream; bench.py uses it to separate a clock
- * ramp from a change in cycles per call.  out: uint64 [2 * (slot + 1)].
- * ------------------------------------------------------------------- */
-int cast_clock_sample(uint64_t *out, int32_t slot, int32_t iters, cast_stream_t stream);
-
-/* ---------------------------------------------------------------------
- * Measurement aid, no counterpart in the reference.  The MFMA ceiling at
- * the bf16 attention kernel's launch shape: `grid` workgroups of 512
- * threads at two waves per SIMD, each wave running `tiles` rounds of that
- * kernel's 32 v_mfma_f32_32x32x16_bf16 per 64-key tile (32768 FLOP each)
- * with no softmax and no global loads.  mode 0: operands in registers;
- * 1: every A operand read from LDS at the kernel's K / V^T addresses;
- * 3: those reads plus the per-tile workgroup barrier.
- *   src   bf16 operand values, src_chunks 16-byte chunks (read modulo)
- *   out   float [grid * 512]   the accumulator sums (keeps the work live)
- *   clk   uint64 [2 * grid]    per workgroup: shader cycles, 100 MHz ticks
- * bench.py uses it to state what the matrix pipes sustain on this part
- * next to the attention kernel's rate.
- * ------------------------------------------------------------------- */
-int cast_mfma_ceiling(const void *src, int64_t src_chunks, float *out, uint64_t *clk, int32_t grid,
-                      int32_t tiles, int32_t mode, cast_stream_t stream);
 
 #ifdef __cplusplus
 }

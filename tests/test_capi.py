@@ -27,12 +27,15 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert names == sorted(_lib.SIGNATURES), "ctypes bindings and header disagree"
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.cast_abi_version() == 3
+    # the measurement aids live in bench.py's own library only
+    for n in ("cast_clock_sample", "cast_mfma_ceiling"):
+        assert not hasattr(lib, n), n
+    assert lib.cast_abi_version() == 4
 
 
 def test_status_strings(lib):
-    for code in range(11):
-        assert lib.cast_status_string(code)
+    for code in range(14):
+        assert lib.cast_status_string(code) != b"unknown status", code
     assert b"multiple of KV heads" in lib.cast_status_string(2)
 
 
@@ -118,6 +121,22 @@ def test_store_append_host_validation(lib):
     assert f(*args(dtype=2)) == 4                # dtype (fp64 has no row copy)
     assert f(*args(dtype=9)) == 4
     assert f(*args(B=0)) == 0 and f(*args(layers=0)) == 0
+
+
+def test_store_append_refuses_lengths_written_over_its_inputs(lib):
+    # new_len is written while other workgroups still read store_len,
+    # path_len, src_row and path: any overlap is refused before a launch
+    import ctypes
+    fake = 1 << 20
+    arr = (ctypes.c_void_p * 2)(fake, fake)
+    B = 4
+    src, path, plen, slen = fake + 0x1000, fake + 0x2000, fake + 0x4000, fake + 0x5000
+
+    def call(new_len):
+        return lib.cast_store_append(arr, arr, arr, arr, 2, src, path, 128, plen, slen, new_len, B, 16, 64, 4,
+                                     128, *([8] * 10), 0, None, None)
+    for alias in (slen, plen, src, path, path + 4 * 128 * B - 4, slen - 4 * B + 4, slen + 12):
+        assert call(alias) == 13, hex(alias)
 
 
 def test_store_layout_checked_once_and_rechecked_on_change():
@@ -249,8 +268,11 @@ def test_build_trees_refuses_host_budgets_above_127():
             build_trees(ti, tl, bad)
 
 
-def test_mfma_ceiling_host_validation(lib):
-    # the measurement aid rejects bad arguments before any launch
+def test_mfma_ceiling_host_validation():
+    # bench.py's measurement aid (libcast_bench.so, not the product library)
+    # rejects bad arguments before any launch
+    from bench import bench_lib
+    lib = bench_lib()
     fake = 1 << 20
     assert lib.cast_mfma_ceiling(None, 8, fake, fake, 1, 1, 0, None) == 1
     assert lib.cast_mfma_ceiling(fake, 0, fake, fake, 1, 1, 0, None) == 7

@@ -36,10 +36,14 @@ def _setup(dev, seed, B=5, L=3, Hkv=4, D=128, cap=96, dtype=torch.bfloat16):
     return buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted
 
 
-@pytest.mark.parametrize("case", ["all-rows", "compact", "grow", "fp32-d64", "fp16"])
+@pytest.mark.parametrize("case", ["all-rows", "compact", "grow", "fp32-d64", "fp16", "fp32-d256", "bf16-d256"])
 def test_append_store_matches_reference(gpu, case):
+    # fp32 at head dim 256 has 1024-byte rows: two 512-byte column slices
+    # per (request, layer, head), one workgroup each
     from cast_amd import serving
-    kw = {"fp32-d64": dict(D=64, dtype=torch.float32), "fp16": dict(dtype=torch.float16)}.get(case, {})
+    kw = {"fp32-d64": dict(D=64, dtype=torch.float32), "fp16": dict(dtype=torch.float16),
+          "fp32-d256": dict(D=256, dtype=torch.float32, Hkv=2),
+          "bf16-d256": dict(D=256, Hkv=2)}.get(case, {})
     buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=len(case), **kw)
     B = len(store_len)
     rows = [0, 2, 3] if case == "compact" else list(range(B))
@@ -85,6 +89,53 @@ def test_append_accepted_from_greedy_accept(gpu):
     assert max(accepted) > 1
     for a, b in zip(got_k + got_v, ref[0] + ref[1]):
         assert torch.equal(a, b)
+
+
+def _path_tensors(keep, dev):
+    B = len(keep)
+    path = torch.full((B, 128), -1, dtype=torch.int32, device=dev)
+    for b in range(B):
+        if len(keep[b]) > 1:
+            path[b, :len(keep[b]) - 1] = torch.tensor([k - 1 for k in keep[b][1:]], dtype=torch.int32)
+    plen = torch.tensor([len(k) - 1 for k in keep], dtype=torch.int32, device=dev)
+    return path, plen
+
+
+def test_append_more_layers_than_one_launch(gpu):
+    # 130 layers: three launches of at most 64 layers.  Every launch reads
+    # store_len as the caller passed it; new_len and the overflow flag come
+    # from the first launch only.
+    from cast_amd import serving
+    L, B = 130, 4
+    buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=33, B=B, L=L, Hkv=2, D=64)
+    keep[1] = keep[1] if len(keep[1]) > 1 else [0, 1]
+    accepted[1] = len(keep[1])
+    path, plen = _path_tensors(keep, gpu)
+    cq = torch.tensor(cu_q, dtype=torch.int32, device=gpu)
+    print(f"case append-{L}-layers: B={B} store_len={store_len} accepted={accepted}", flush=True)
+    got_k, got_v = [x.clone() for x in buf_k], [x.clone() for x in buf_v]
+    new_len = serving.append_accepted(got_k, got_v, torch.tensor(store_len, dtype=torch.int32, device=gpu), cq,
+                                      path, plen, pack_k, pack_v, check=True)
+    ref = OS.append_store([x.clone() for x in buf_k], [x.clone() for x in buf_v], pack_k, pack_v, store_len,
+                          cu_q, keep, accepted, list(range(B)))
+    assert new_len.cpu().tolist() == ref[2]
+    for i, (a, b) in enumerate(zip(got_k + got_v, ref[0] + ref[1])):
+        assert torch.equal(a, b), f"layer {i % L} ({'KV'[i // L]})"
+    # request 1 past its capacity: flagged and skipped in every layer, the
+    # other requests appended as before
+    cap = buf_k[0].shape[2]
+    sl = list(store_len)
+    sl[1] = cap - 1
+    print(f"case append-{L}-layers-overflow: store_len={sl}", flush=True)
+    flag_k, flag_v = [x.clone() for x in buf_k], [x.clone() for x in buf_v]
+    with pytest.raises(ValueError, match="inconsistent"):
+        serving.append_accepted(flag_k, flag_v, torch.tensor(sl, dtype=torch.int32, device=gpu), cq, path, plen,
+                                pack_k, pack_v, check=True)
+    for i in range(2 * L):
+        got, old, want = (flag_k + flag_v)[i], (buf_k + buf_v)[i], (got_k + got_v)[i]
+        assert torch.equal(got[1], old[1]), f"layer {i % L}: the flagged request was written"
+        for b in (0, 2, 3):
+            assert torch.equal(got[b], want[b]), f"layer {i % L} request {b}"
 
 
 def test_append_overflow_is_flagged(gpu):
@@ -162,11 +213,7 @@ def test_append_from_hook_record_matches_explicit_packs(gpu):
     from cast_amd import serving
     buf_k, buf_v, pack_k, pack_v, store_len, cu_q, keep, accepted = _setup(gpu, seed=21)
     B, L = len(store_len), len(buf_k)
-    path = torch.full((B, 128), -1, dtype=torch.int32, device=gpu)
-    for b in range(B):
-        if len(keep[b]) > 1:
-            path[b, :len(keep[b]) - 1] = torch.tensor([k - 1 for k in keep[b][1:]], dtype=torch.int32)
-    plen = torch.tensor([len(k) - 1 for k in keep], dtype=torch.int32, device=gpu)
+    path, plen = _path_tensors(keep, gpu)
     sl = torch.tensor(store_len, dtype=torch.int32, device=gpu)
     cq = torch.tensor(cu_q, dtype=torch.int32, device=gpu)
     print(f"case append-hook-record: B={B} L={L}", flush=True)

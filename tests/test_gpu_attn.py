@@ -26,11 +26,11 @@ def _words(wl):
 
 
 def _run_and_check(wl, dev, requests=None, kv_heads=None, kv_split=0, one_word=False, q_noncontig=False,
-                   label=""):
+                   label="", qkv=None, reference_bar=False):
     from cast_amd import varlen_tree_attention
     print(f"case {label or wl.name}: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv} "
           f"Hq={wl.Hq} Hkv={wl.Hkv} D={wl.D} {wl.dtype} split={kv_split}", flush=True)
-    q, k, v = wl.qkv(device=dev)
+    q, k, v = wl.qkv(device=dev) if qkv is None else (x.to(dev) for x in qkv)
     words = _words(wl)
     if one_word:
         assert not words[:, 1].any()
@@ -53,6 +53,9 @@ def _run_and_check(wl, dev, requests=None, kv_heads=None, kv_split=0, one_word=F
     err_l = (got_l - ref_l).abs()[sel & torch.isfinite(ref_l)]
     tol = TOL[wl.dtype]
     print(f"  out max {err_o.max():.3e} mean {err_o.mean():.3e}  lse max {err_l.max():.3e}", flush=True)
+    if reference_bar:
+        # the reference kernel test's own assertion (tests/test_tree_attn.py:73-74)
+        assert err_o.max().item() < 5e-2 and err_o.mean().item() < 5e-3
     assert torch.isfinite(got_o[sel]).all()
     assert err_o.max() <= tol["out"] and err_o.mean() <= tol["mean"]
     assert err_l.max() <= tol["lse"]
@@ -66,6 +69,20 @@ def test_reference_scenario(gpu, dtype):
     wl = SC.random_parent_batch(seed=0, dtype=dtype)
     _run_and_check(wl, gpu, label=f"reference-scenario-{dtype}")
     _run_and_check(wl, gpu, one_word=True, label=f"reference-scenario-{dtype}-int64-mask")
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_reference_kernel_test_tensors(gpu, dtype):
+    # the reference kernel test's exact tensors (same generator, same draw
+    # order), cast to the dtype as it does (tests/test_tree_attn.py:64-72),
+    # with its one-word int64 mask; the oracle runs on the rounded inputs in
+    # fp32 as its dense reference does.  Both its bar and the tighter one.
+    import dataclasses
+    wl, q, k, v = SC.reference_test_batch(seed=0)
+    wl = dataclasses.replace(wl, dtype=dtype)
+    dt = SC.torch_dtype(dtype)
+    _run_and_check(wl, gpu, one_word=True, qkv=(q.to(dt), k.to(dt), v.to(dt)), reference_bar=True,
+                   label=f"reference-kernel-test-{dtype}")
 
 
 def test_cpu_plumbing_config(gpu):

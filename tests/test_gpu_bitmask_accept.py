@@ -77,6 +77,19 @@ def test_accept_planted_paths_small_vocab(gpu):
     _accept_case(wl, logits.float(), gpu, "planted-fp32")
 
 
+@pytest.mark.parametrize("seed,accept_p", [(0, 0.8), (1, 0.8), (8, 1.0), (34, 1.0)])
+def test_accept_cpu_plumbing_config(gpu, seed, accept_p):
+    # the CPU-plumbing configuration's own leg: its N=15 tree (15 x 64 block
+    # of N(0,5) scores, seed 0, cast_trees examples/quickstart.py:12) and
+    # planted [16, 64] fp32 verify logits (walk of cast_trees/decode.py:96-103)
+    wl = SC.cpu_plumbing()
+    logits, planted = SC.planted_logits(wl, vocab=64, seed=seed, accept_p=accept_p)
+    assert logits.shape == (16, 64) and logits.dtype == torch.float32
+    ref = _accept_case(wl, logits, gpu, f"cpu-plumbing-seed{seed}")
+    assert [p for p, _ in ref] == planted
+    _accept_case(wl, logits.to(torch.bfloat16), gpu, f"cpu-plumbing-seed{seed}-bf16")
+
+
 def test_accept_full_vocab_with_ties_and_nan(gpu):
     wl = SC.qwen3_ragged(seed=5, B=3, lo=1, hi=2, packs=(16, 32))
     logits, _ = SC.planted_logits(wl, seed=5, accept_p=0.9)

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+from bench import bench_lib
 from cast_amd import _lib
 
 pytestmark = pytest.mark.gpu
@@ -53,7 +54,7 @@ def _expected_wave(src, wave, tiles, mode):
 
 @pytest.mark.parametrize("mode", [0, 1, 3])
 def test_mfma_ceiling_does_the_products_it_claims(gpu, mode):
-    lib = _lib.load()
+    lib = bench_lib()
     grid, tiles = 2, 3                                   # odd: both LDS tile buffers are read
     g = torch.Generator(device=gpu).manual_seed(11)
     src = torch.randn(40000 * 8, generator=g, device=gpu).to(torch.bfloat16)   # 40000 chunks, read modulo
@@ -77,7 +78,7 @@ def test_mfma_ceiling_does_the_products_it_claims(gpu, mode):
 
 
 def test_clock_sample_reads_a_plausible_clock(gpu):
-    lib = _lib.load()
+    lib = bench_lib()
     buf = torch.zeros(8, dtype=torch.int64, device=gpu)
     for slot in range(4):
         _lib.check(lib.cast_clock_sample(_lib.ptr(buf), slot, 20000, _lib.stream_of(buf)), "cast_clock_sample")

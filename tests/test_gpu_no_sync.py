@@ -48,3 +48,37 @@ def test_round_steps_do_not_sync(gpu):
     finally:
         torch.cuda.set_sync_debug_mode("default")
     torch.cuda.synchronize()
+
+
+def test_batch_one_tree_hook_does_not_sync(gpu):
+    # the "cast_tree" attention of the batch-one verify (cast_trees/decode.py:
+    # 166-171): the mask from tree_attention_mask carries its kernel metadata,
+    # so building it and running the hook for several layers never waits on
+    # the device.  The result is then checked against SDPA with the same mask.
+    from cast_amd import serving
+    from cast_amd.verify import tree_attention_mask
+    wl = SC.qwen3_single(seed=3, prefix=300, pack=40)
+    nodes, S, n = wl.trees[0], 300, 40
+    Hq, Hkv, D = wl.Hq, wl.Hkv, wl.D
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q = torch.randn((1, Hq, n, D), generator=g, device=gpu).to(torch.bfloat16)
+    key = torch.randn((1, Hkv, S + n, D), generator=g, device=gpu).to(torch.bfloat16)
+    value = torch.randn((1, Hkv, S + n, D), generator=g, device=gpu).to(torch.bfloat16)
+    print(f"case no-sync batch-one hook: S={S} n={n}", flush=True)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        mask = tree_attention_mask(S, nodes, gpu, torch.bfloat16)
+        outs = [serving._tree_attention(None, q, key, value, mask, scaling=D ** -0.5)[0] for _ in range(3)]
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, outs[0]) for o in outs)
+    G = Hq // Hkv
+    kf = key.float().cpu().repeat_interleave(G, 1)
+    vf = value.float().cpu().repeat_interleave(G, 1)
+    want = torch.nn.functional.scaled_dot_product_attention(q.float().cpu(), kf, vf,
+                                                            attn_mask=mask.float().cpu(), scale=D ** -0.5)
+    err = (outs[0].float().cpu() - want.transpose(1, 2)).abs().max().item()
+    print(f"  out max err {err:.3e}", flush=True)
+    assert err <= 2e-2

@@ -21,7 +21,7 @@ from oracle import bitmask as OB
 pytestmark = pytest.mark.gpu
 
 
-def _setup(gpu, packs, prefix, seed=0):
+def _setup(gpu, packs, prefix, seed=0, D=128):
     from cast_amd.tree import TreeNode
     rng = np.random.default_rng(seed)
     trees = []
@@ -33,7 +33,7 @@ def _setup(gpu, packs, prefix, seed=0):
             depth[i] = depth[par[i]] + 1
             nodes.append(TreeNode(int(rng.integers(0, 1000)), depth[i], par[i] - 1, 0.0))
         trees.append(nodes)
-    wl = SC._make("rejects", trees, prefix, dict(Hq=16, Hkv=4, D=128, vocab=1000), "bf16", seed, 1 / math.sqrt(128))
+    wl = SC._make("rejects", trees, prefix, dict(Hq=16, Hkv=4, D=D, vocab=1000), "bf16", seed, 1 / math.sqrt(D))
     q, k, v = wl.qkv(device=gpu)
     words = OB.chain_walk_words(wl.packed.parent, wl.cu_q)
     return wl, q, k, v, words
@@ -142,14 +142,32 @@ def test_store_batch_above_total_kv(gpu, kv_split):
     assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
 
 
-def test_fp32_generic_path_rejects_too(gpu):
+def test_fp32_mfma_kernel_rejects_too(gpu):
+    # fp32 at head dim 128: tree_attn_f32_kernel
     from cast_amd import varlen_tree_attention
     wl, q, k, v, words = _setup(gpu, [10, 100, 20], [300, 50, 700], seed=4)
     q, k, v = q.float(), k.float(), v.float()
-    print("case reject-long-pack-fp32", flush=True)
+    print("case reject-long-pack-fp32-mfma", flush=True)
     meta = wl.meta_tensors(gpu)
     one_word = torch.from_numpy(words[:, 0].view(np.int64).copy()).to(gpu)
     out = _poison(torch.empty_like(q))
+    out, lse = varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                                     one_word, return_lse=True, out=out)
+    _check(wl, q, k, v, words, out, lse, accepted=[0, 2])
+
+
+@pytest.mark.parametrize("dtype,D", [("bf16", 96), ("fp32", 96), ("bf16", 192)])
+def test_scalar_kernel_rejects_too(gpu, dtype, D):
+    # head dims off the MFMA kernels take tree_attn_generic_kernel: its
+    # batch prologue zero-fills the rejected request's rows the same way
+    from cast_amd import varlen_tree_attention
+    wl, q, k, v, words = _setup(gpu, [10, 100, 20], [300, 50, 700], seed=6, D=D)
+    if dtype == "fp32":
+        q, k, v = q.float(), k.float(), v.float()
+    print(f"case reject-long-pack-scalar-{dtype}-D{D}", flush=True)
+    meta = wl.meta_tensors(gpu)
+    one_word = torch.from_numpy(words[:, 0].view(np.int64).copy()).to(gpu)
+    out, lse = _poison(torch.empty_like(q)), _poison(torch.empty(q.shape[:2], device=gpu))
     out, lse = varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
                                      one_word, return_lse=True, out=out)
     _check(wl, q, k, v, words, out, lse, accepted=[0, 2])

@@ -122,3 +122,19 @@ def test_pack_trees_layout_and_errors():
     bad = [T.TreeNode(1, 1, -1, 0.0), T.TreeNode(2, 2, 1, 0.0)]
     with pytest.raises(ValueError):
         T.pack_trees([bad])
+
+
+@pytest.mark.parametrize("budget", [0, 15, 63, 64, 127])
+def test_host_ancestor_words_are_the_chain_walk_words(budget):
+    # the words the batch-one mask carries for the "cast_tree" kernel equal
+    # the oracle's chain walk (word 0 is the reference's int64 recurrence)
+    from cast_amd.verify import ancestor_words
+    from oracle import bitmask as OB
+    idx, lp = T.block_topk(np.random.default_rng(budget).normal(scale=2, size=(15, 200)), 8)
+    nodes = T.build_tree(idx, lp, budget=budget)
+    pk = T.pack_trees([nodes])
+    got = ancestor_words(T.ancestor_matrix(nodes))
+    assert got.dtype == np.int64 and got.shape == (budget + 1, 2)
+    assert np.array_equal(got, OB.chain_walk_words(pk.parent, pk.cu_q).view(np.int64))
+    with pytest.raises(ValueError):
+        ancestor_words(np.ones((129, 129), dtype=bool))

@@ -26,6 +26,59 @@ def _args(wl, dev, q, k, v, out, lse, mask, meta, kv_split):
             v.stride(0), v.stride(1), out.stride(0), out.stride(1), _DT[wl.dtype], float(wl.D ** -0.5), kv_split]
 
 
+def test_noalloc_first_call_under_graph_capture(gpu):
+    # Run in file order, this is the process's first call of the no-alloc
+    # entry point, so the scratch address lookup (hipGetSymbolAddress) runs
+    # inside a HIP graph capture.  The graph is replayed on three sets of
+    # inputs, with eager work between the replays, each bit for bit equal
+    # to the workspace entry on the same inputs.
+    lib = _lib.load()
+    wl = SC.qwen3_ragged(seed=4, B=3, lo=200, hi=2000)
+    kv_split = 256
+    q, k, v = wl.qkv(device=gpu)
+    meta = wl.meta_tensors(gpu)
+    mask = torch.from_numpy(OB.chain_walk_words(wl.packed.parent, wl.cu_q).view(np.int64).copy()).to(gpu)
+    need = lib.cast_tree_attn_workspace_size(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D, _DT[wl.dtype],
+                                             kv_split)
+    print(f"case noalloc-graph-capture: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv} scratch {need} B",
+          flush=True)
+    assert 0 < need <= lib.cast_tree_attn_noalloc_limit()
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    out_g, out_r = torch.empty_like(q), torch.empty_like(q)
+    lse_g = torch.empty(q.shape[:2], device=gpu)
+    lse_r = torch.empty_like(lse_g)
+    status = torch.zeros(2, dtype=torch.int32, device=gpu)
+
+    def workspace_entry():
+        with torch.cuda.device(gpu):
+            st = lib.cast_tree_attn_fwd(*_args(wl, gpu, q, k, v, out_r, lse_r, mask, meta, kv_split), _lib.ptr(ws),
+                                        need, _lib.ptr(status[1:2]), _lib.stream_of(q))
+        assert st == 0, _lib.status_string(st)
+
+    workspace_entry()          # eager: the kernels' code object is loaded before the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.device(gpu), torch.cuda.graph(graph):
+        st = lib.cast_tree_attn_fwd_noalloc(*_args(wl, gpu, q, k, v, out_g, lse_g, mask, meta, kv_split),
+                                            _lib.ptr(status[0:1]), _lib.stream_of(q))
+    assert st == 0, _lib.status_string(st)
+    gen = torch.Generator(device=gpu).manual_seed(11)
+    for rep in range(3):
+        if rep:
+            for t in (q, k, v):
+                t.copy_(torch.randn(t.shape, generator=gen, device=gpu).to(t.dtype))
+        out_g.fill_(float("nan"))
+        lse_g.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        workspace_entry()
+        torch.cuda.synchronize()
+        print(f"  replay {rep}", flush=True)
+        assert status.tolist() == [0, 0]
+        assert torch.isfinite(out_g).all() and torch.isfinite(lse_g).all()
+        assert torch.equal(out_g, out_r) and torch.equal(lse_g, lse_r), f"replay {rep}"
+
+
 def _both(gpu, wl, kv_split=0):
     lib = _lib.load()
     q, k, v = wl.qkv(device=gpu)
