@@ -83,6 +83,10 @@ struct AttnArgs {
     int32_t chunk;      // keys per split, multiple of 64 (kNoSplit = no split)
     int32_t max_rows;   // longest key source (rows) the MFMA kernel can address
     int32_t xcds;       // XCDs of the device: workgroup x runs on XCD x % xcds
+    int32_t sk_mode;    // stream-K schedule asked for (CAST_SPLIT_STREAM)
+    int32_t sk_wgs;     // stream-K workgroups (resident at once; a multiple of 2 * xcds)
+    int32_t sk_min_tiles;   // shortest stream-K lane (key tiles)
+    float *sk_lse;      // stream-K partial lse [2 * sk_wgs][rows_wg] (partial O at part_o)
     int32_t rows_wg;    // query rows per workgroup
     int32_t comb_groups;  // combine kernel: head groups per packed token
     float *part_o;      // [part_rows][Hq][D] fp32, normalised partial outputs
@@ -421,11 +425,12 @@ __device__ __forceinline__ uint32_t vis_window(uint64_t w0, uint64_t w1, int j0)
 // so that it holds no scalar registers there.
 struct EpiArgs {
     void *out;
-    float *lse, *part_o, *part_lse;
+    float *lse, *part_o, *part_lse, *sk_lse;
     int32_t *status;
     int64_t o_tok, o_head, part_rows;
-    int64_t prow0;      // partial row of token q0 + i is prow0 + q0 + i
-    int32_t ns, Hq;
+    int64_t prow0;      // static partial row of token q0 + i is prow0 + q0 + i
+    int32_t slot;       // stream-K partial slot (-1: static)
+    int32_t final_out, Hq;
 };
 
 // Raw buffer resource over `rows` key rows of `row_bytes` stride and
@@ -440,12 +445,169 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
-// The unit of the calling workgroup, after the batch prologue; false when
-// the workgroup has none (or the batch was rejected).  Batches of up to 64
-// requests use the longest-first schedule; larger ones take items in batch
-// order, consecutive items (the row blocks of one key split) on one XCD
-// (workgroups are dealt to the XCDs round-robin) so that they share its L2.
-__device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, int &split, int &rb) {
+// ---- stream-K schedule ("lanes"), batches of up to 64 requests.  The
+// static schedule above cuts every request into equal key splits; when the
+// requests' lengths differ, its longest item sets the call's time while
+// other CUs idle.  Stream-K gives every lane the same number of key tiles
+// instead:
+//  - a lane is two workgroups on one XCD (x and x + xcds);
+//  - the units of request b - (KV head h, row block r), unit index
+//    k = h * rb + r - are paired into super-groups (2s, 2s + 1): the two row
+//    blocks of one head (they read the same keys, which the lane's two
+//    workgroups then share through the XCD's L2), or two heads when a head
+//    has one row block;
+//  - a super-group is tiles_b lane-steps (the request's key tiles: its
+//    prefix in 64-key tiles, then its pack); the super-groups of all
+//    requests, in batch order, make a line of C lane-steps, and lane l takes
+//    steps [l * L, (l + 1) * L), L = ceil(C / lanes);
+//  - member m of a lane runs unit 2s + m of every super-group its range
+//    touches, over the key tiles the range covers, carrying the online
+//    softmax across consecutive tiles.  A segment that covers its unit's
+//    whole key range writes the output; the lane's first and last segments
+//    otherwise write a partial (O, lse) into slot 2x or 2x + 1 of workgroup
+//    x, which the combine kernel merges.
+constexpr int kSkMaxPieces = 64;   // lanes one unit may span (the combine's LDS tables)
+
+// A request's stream-K figures, shared through LDS during the segment loop.
+struct SkReq {
+    int base, cost, tiles, npre, rb, units, S, P, q0, kv0;
+};
+
+struct SkPlan {
+    bool use;
+    int C, L;
+};
+
+// Key tiles of a request: its prefix in 64-key tiles, then its pack.
+__device__ __forceinline__ int seq_tiles_pre(const Seq &t) { return (t.S + 63) >> 6; }
+__device__ __forceinline__ int seq_tiles(const Seq &t) { return ((t.S + 63) >> 6) + ((t.P + 63) >> 6); }
+
+// The wave's maximum, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+    for (int off = 32; off; off >>= 1) x = max(x, __shfl_xor(x, off));
+    return __builtin_amdgcn_readfirstlane(x);
+}
+
+// Lane and member of workgroup x, and back: the two members of a lane run
+// on one XCD (workgroups are dealt to the XCDs round-robin).
+__device__ __forceinline__ int sk_lane_of(int x, int nx, int &member) {
+    const int k = x / nx;
+    member = k & 1;
+    return (k >> 1) * nx + x % nx;
+}
+__device__ __forceinline__ int sk_wg_of(int lane, int member, int nx) {
+    return ((lane / nx) * 2 + member) * nx + lane % nx;
+}
+
+// Per-lane stream-K figures of request `lane` (t, loaded when it passed
+// load_seq) and the batch's plan; every workgroup of the attention and
+// combine kernels computes the same plan from the same metadata.  The
+// static schedule stays when a unit would span more than kSkMaxPieces
+// lanes.
+__device__ SkPlan sk_plan(const AttnArgs &a, const Seq &t, bool ok, int &base, int &cost, int &tiles) {
+    const bool has = ok && t.P > 0;
+    tiles = has ? seq_tiles(t) : 0;
+    const int units = has ? a.Hkv * t.rb : 0;
+    cost = sat32((int64_t)((units + 1) >> 1) * tiles);
+    const int C = wave_sum(cost);
+    base = wave_scan(cost) - cost;
+    SkPlan pl{false, C, 0};
+    const int lanes = a.sk_wgs >> 1;
+    if (a.sk_mode == 0 || lanes == 0 || C <= 0 || C == 0x7fffffff) return pl;
+    pl.L = max((C + lanes - 1) / lanes, a.sk_min_tiles);
+    pl.use = wave_max(tiles) <= (kSkMaxPieces - 2) * pl.L;
+    return pl;
+}
+
+// One piece of work: query rows [rb * rows_wg, +rows_wg) of (request sq, KV
+// head h) against its keys [k_begin, k_end), and where the result goes:
+// the output (final), a static split-K partial (partial row of token q0 + i
+// at prow0 + q0 + i, [part_rows][Hq][D]), or stream-K slot `slot`
+// ([2 * sk_wgs][rows_wg][D]).
+struct Unit {
+    Seq sq;
+    int h, rb, k_begin, k_end;
+    int64_t prow0;
+    int slot;
+    bool final_out;
+};
+
+// Where a workgroup is in its stream-K lane.
+struct WorkCursor {
+    int64_t p, end, start;   // lane-steps: next position, lane end, lane start
+    int member, x;
+    bool sk;
+};
+
+// The next segment of the lane from cur.p on whose unit exists (a member
+// whose super-group has one unit idles there); false at the lane's end.
+__device__ bool sk_next_segment(const AttnArgs &a, WorkCursor &cur, Unit &u, const SkReq *skr) {
+    const int lane = threadIdx.x & 63;
+    const bool in = lane < a.batch;
+    const int my_base = in ? skr[lane].base : 0, my_cost = in ? skr[lane].cost : 0;
+    while (cur.p < cur.end) {
+        const int64_t p = cur.p;
+        const uint64_t hit = __ballot(in && my_cost > 0 && p >= my_base && p < (int64_t)my_base + my_cost);
+        if (!hit) return false;
+        const int b = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
+        // wave-uniform values, kept in scalar registers
+        SkReq q = skr[b];
+        q.base = __builtin_amdgcn_readfirstlane(q.base);
+        q.cost = __builtin_amdgcn_readfirstlane(q.cost);
+        q.tiles = __builtin_amdgcn_readfirstlane(q.tiles);
+        q.npre = __builtin_amdgcn_readfirstlane(q.npre);
+        q.rb = __builtin_amdgcn_readfirstlane(q.rb);
+        q.units = __builtin_amdgcn_readfirstlane(q.units);
+        q.S = __builtin_amdgcn_readfirstlane(q.S);
+        q.P = __builtin_amdgcn_readfirstlane(q.P);
+        q.q0 = __builtin_amdgcn_readfirstlane(q.q0);
+        q.kv0 = __builtin_amdgcn_readfirstlane(q.kv0);
+        const int rel = (int)(p - q.base);
+        const int sgi = rel / q.tiles, off = rel % q.tiles;
+        const int64_t seg_end = min(cur.end, (int64_t)q.base + (int64_t)(sgi + 1) * q.tiles);
+        const int n = (int)(seg_end - p);
+        const int k = 2 * sgi + cur.member;
+        const bool first = p == cur.start;
+        cur.p = seg_end;
+        if (k >= q.units) continue;
+        Seq &sq = u.sq;
+        sq.b = b;
+        sq.S = q.S;
+        sq.P = q.P;
+        sq.T = q.S + q.P;
+        sq.q0 = q.q0;
+        sq.kv0 = q.kv0;
+        sq.ns = 1;
+        sq.rb = q.rb;
+        sq.split_len = 0;
+        sq.part_off = 0;
+        u.h = k / q.rb;
+        u.rb = k % q.rb;
+        // tiles [off, off + n): prefix tiles first, then pack tiles from S
+        auto key0 = [&](int i) { return i < q.npre ? i * 64 : q.S + (i - q.npre) * 64; };
+        auto key1 = [&](int i) { return i < q.npre ? min(i * 64 + 64, q.S) : min(q.S + (i - q.npre) * 64 + 64, sq.T); };
+        u.k_begin = key0(off);
+        u.k_end = key1(off + n - 1);
+        u.final_out = off == 0 && n == q.tiles;
+        u.slot = u.final_out ? -1 : 2 * cur.x + (first ? 0 : 1);
+        u.prow0 = 0;
+        return true;
+    }
+    return false;
+}
+
+// The first piece of work of the calling workgroup, after the batch
+// prologue; false when it has none (or the batch was rejected).  Batches of
+// up to 64 requests take the stream-K lanes when sk_plan chooses them, else
+// the longest-first schedule; larger ones take items in batch order,
+// consecutive items (the row blocks of one key split) on one XCD so that
+// they share its L2.  skr: LDS for the stream-K table (64 entries).
+template <bool SK>   // SK: the kernel instance takes the stream-K schedule when the plan asks
+__device__ bool first_unit(const AttnArgs &a, WorkCursor &cur, Unit &u, SkReq *skr) {
+    cur.sk = false;
+    Seq &sq = u.sq;
+    int h = 0, split = 0, rb = 0;
     if (a.batch <= 64) {
         // one round of metadata loads serves the totals and the schedule
         const int lane = threadIdx.x & 63;
@@ -454,23 +616,57 @@ __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, 
         BatchTotals tot{0, 0, 0, false, false};
         add_totals(tot, a, lane, ok, t);
         if (!batch_prologue(a, tot)) return false;
-        return locate_sorted(a, blockIdx.x, t, ok, sq, h, split, rb);
+        int base, cost, tiles;
+        const SkPlan pl = SK ? sk_plan(a, t, ok, base, cost, tiles) : SkPlan{false, 0, 0};
+        if (SK && pl.use) {
+            if (threadIdx.x < 64 && lane < a.batch)
+                skr[lane] = SkReq{base, cost, tiles, ok ? seq_tiles_pre(t) : 0, ok ? t.rb : 0,
+                                  ok && t.P > 0 ? a.Hkv * t.rb : 0, t.S, t.P, t.q0, t.kv0};
+            __syncthreads();
+            const int x = blockIdx.x;
+            if (x >= a.sk_wgs) return false;
+            int member;
+            const int l = sk_lane_of(x, a.xcds, member);
+            cur.sk = true;
+            cur.member = member;
+            cur.x = x;
+            cur.start = cur.p = (int64_t)l * pl.L;
+            cur.end = min(cur.p + pl.L, (int64_t)pl.C);
+            return sk_next_segment(a, cur, u, skr);
+        }
+        if (!locate_sorted(a, blockIdx.x, t, ok, sq, h, split, rb)) return false;
+    } else {
+        const BatchTotals tot = batch_totals(a);
+        if (!batch_prologue(a, tot)) return false;
+        const int64_t total = tot.items;
+        const int nx = a.xcds;
+        const int64_t n8 = (total + nx - 1) / nx * nx;
+        const int64_t x = blockIdx.x;
+        if (x >= n8) return false;
+        const int64_t w = (x % nx) * (n8 / nx) + x / nx;
+        if (w >= total) return false;
+        int local;
+        if (!find_request(a, w, false, sq, local)) return false;
+        rb = local % sq.rb;
+        split = (local / sq.rb) % sq.ns;
+        h = local / (sq.rb * sq.ns);
     }
-    const BatchTotals tot = batch_totals(a);
-    if (!batch_prologue(a, tot)) return false;
-    const int64_t total = tot.items;
-    const int nx = a.xcds;
-    const int64_t n8 = (total + nx - 1) / nx * nx;
-    const int64_t x = blockIdx.x;
-    if (x >= n8) return false;
-    const int64_t w = (x % nx) * (n8 / nx) + x / nx;
-    if (w >= total) return false;
-    int local;
-    if (!find_request(a, w, false, sq, local)) return false;
-    rb = local % sq.rb;
-    split = (local / sq.rb) % sq.ns;
-    h = local / (sq.rb * sq.ns);
+    u.h = h;
+    u.rb = rb;
+    u.k_begin = split * sq.split_len;
+    u.k_end = min(sq.T, u.k_begin + sq.split_len);
+    u.final_out = sq.ns == 1;
+    u.slot = -1;
+    u.prow0 = sq.part_off + (int64_t)split * sq.P - sq.q0;
     return true;
+}
+
+// The workgroup's next piece of work (stream-K lanes only), after a
+// barrier that retires the previous piece's use of LDS.
+__device__ __forceinline__ bool next_unit(const AttnArgs &a, WorkCursor &cur, Unit &u, const SkReq *skr) {
+    if (!cur.sk || cur.p >= cur.end) return false;
+    __syncthreads();
+    return sk_next_segment(a, cur, u, skr);
 }
 
 // WPE: waves per SIMD the register budget is sized for.  2 (256 registers a
@@ -480,7 +676,10 @@ __device__ __forceinline__ bool locate_item(const AttnArgs &a, Seq &sq, int &h, 
 // threads each stage four times the 8-wave instance's share of a K tile
 // (about 330 registers): its 72 KB of LDS allow two such workgroups per
 // CU, one wave per SIMD, either way.
-template <int D, int WAVES, bool STORE, typename E, int WPE = 2>
+// SKI: the stream-K instance (a run of segments per workgroup, the next
+// segment's first tile and Q loaded during a segment's last tile); the
+// static instances do one unit each.
+template <int D, int WAVES, bool STORE, typename E, int WPE = 2, bool SKI = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void tree_attn_mfma_kernel(AttnArgs a) {
     using vec8 = typename E::vec8;
@@ -504,72 +703,42 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[NBUF][BN * KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[NBUF][D * VPAD];
     __shared__ EpiArgs epi;
+    // Head dim 256 (one wave per SIMD, no registers to spare) has no
+    // stream-K instance.
+    constexpr bool kStreamK = SKI && D <= 128;
+    __shared__ SkReq skr[kStreamK ? 64 : 1];
 
-    // ---- which unit is this workgroup?
-    Seq sq;
-    int rb, split, h;
-    if (!locate_item(a, sq, h, split, rb)) return;
-    const int k_begin = split * sq.split_len;
-    const int k_end = min(sq.T, k_begin + sq.split_len);
-
+    // ---- this workgroup's work: one unit, or a run of stream-K segments
+    Unit wu;
+    WorkCursor cur;
+    if (!first_unit<kStreamK>(a, cur, wu, skr)) return;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const int g = lane >> 5;
     const int l32 = lane & 31;
-    const int rows = sq.P * a.G;
-    const int r = rb * ROWS + wave * 32 + l32;     // this lane's query row
-    const bool active = rb * ROWS + wave * 32 < rows;
-    const bool qvalid = r < rows;
-    const int qtok = sq.q0 + (qvalid ? r / a.G : 0);
-    const int qhead = h * a.G + (qvalid ? r % a.G : 0);
-
     const uint16_t *qp = static_cast<const uint16_t *>(a.q);
-    const KvView<uint16_t> kv(a.kv, sq, h);
 
     // ---- Q^T operand (B side): query l32, head-dim slice [ds*16 + g*8, +8)
+    // of this lane's row of unit w
     vec8 qreg[DSTEPS];
-    {
-        const uint16_t *src = qp + (int64_t)qtok * a.q_tok + (int64_t)qhead * a.q_head + g * 8;
+    auto load_q = [&](const Unit &w) __attribute__((always_inline)) {
+        const int r = w.rb * ROWS + wave * 32 + l32;
+        const bool valid = r < w.sq.P * a.G;
+        const int tok = w.sq.q0 + (valid ? r / a.G : 0);
+        const int head = w.h * a.G + (valid ? r % a.G : 0);
+        const uint16_t *src = qp + (int64_t)tok * a.q_tok + (int64_t)head * a.q_head + g * 8;
 #pragma unroll
         for (int ds = 0; ds < DSTEPS; ++ds)
-            qreg[ds] = qvalid ? *reinterpret_cast<const vec8 *>(src + ds * 16) : vec8{};
-    }
-    uint64_t mw0 = 0, mw1 = 0;
-    if (qvalid && k_end > sq.S) {
-        const uint64_t *mp = a.mask + (int64_t)qtok * a.mask_words;
-        mw0 = mp[0];
-        if (a.mask_words > 1) mw1 = mp[1];
-    }
+            qreg[ds] = valid ? *reinterpret_cast<const vec8 *>(src + ds * 16) : vec8{};
+    };
 
-    floatx16 o[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db) o[db] = floatx16{};
-    float m = -INFINITY, msafe = 0.f, lsum = 0.f;
-    const float c = a.scale_log2;
-
-    // ---- key tiles, each covering keys [t0, t0 + valid), valid <= BN (the
-    // rest of the tile is masked).  The split's prefix keys [k_begin, pre_end)
-    // and pack keys [pk_begin, k_end) are tiled separately: in the store
-    // layout every tile then reads one source, and both layouts add up the
-    // same keys in the same order.
-    const int pre_end = min(k_end, sq.S);
-    const int n_pre = k_begin < pre_end ? (pre_end - k_begin + BN - 1) / BN : 0;
-    const int pk_begin = max(k_begin, sq.S);
-    const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
-    const int ntiles = n_pre + n_pack;
-    auto tile_t0 = [&](int t) __attribute__((always_inline)) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
-    auto tile_valid = [&](int t) __attribute__((always_inline)) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
-
-    // ---- global -> register staging of one tile.  Each key source of this
+    // ---- global -> register staging of one tile.  Each key source of a
     // (request, head) is one buffer resource that ends at its last row (the
     // concat layout: the request's S+P rows; the store layout: its S prefix
     // slots and its P pack rows), so rows past it read as zeros; a tile adds
     // 32-bit byte offsets (row * row stride + 16-byte chunk).  Rows past a
     // split's end but inside the request are real keys, masked below.
-    const uint32_t ksb_pre = (uint32_t)kv.kpre_t * 2u, vsb_pre = (uint32_t)kv.vpre_t * 2u;
-    const uint32_t ksb_pack = (uint32_t)kv.kpack_t * 2u, vsb_pack = (uint32_t)kv.vpack_t * 2u;
-    const int rows_pre = STORE ? sq.S : sq.T;
     u32x4 kst[K_PER_T];
     u32x4 vst[V_PER_T][8];
     // loads of one tile from one source (base, rows, byte strides); row0 is
@@ -597,16 +766,68 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                 vst[it][i] = load16(vrs, __umul24(v0 + 8 * (i >> 2) + (i & 3), vsb) + dch * 16);
         }
     };
-    // the source is chosen by a (wave-uniform) branch, not by selecting
-    // between the two sources' values, which the compiler may lower to
-    // loads through a private array
-    auto fetch = [&](int t) __attribute__((always_inline)) {
-        const int t0 = tile_t0(t);
-        if (!STORE || t < n_pre)
-            fetch_from(kv.kpre, kv.vpre, rows_pre, ksb_pre, vsb_pre, (uint32_t)t0);
+    // the tile of keys [t0, t0 + 64) of (request q, head view v): its source
+    // is chosen by a (wave-uniform) branch, not by selecting between the two
+    // sources' values, which the compiler may lower to loads through a
+    // private array
+    auto fetch_tile = [&](const KvView<uint16_t> &v, const Seq &q, int t0) __attribute__((always_inline)) {
+        if (!STORE || t0 < q.S)
+            fetch_from(v.kpre, v.vpre, STORE ? q.S : q.T, (uint32_t)v.kpre_t * 2u, (uint32_t)v.vpre_t * 2u,
+                       (uint32_t)t0);
         else
-            fetch_from(kv.kpack, kv.vpack, sq.P, ksb_pack, vsb_pack, (uint32_t)(t0 - sq.S));
+            fetch_from(v.kpack, v.vpack, q.P, (uint32_t)v.kpack_t * 2u, (uint32_t)v.vpack_t * 2u,
+                       (uint32_t)(t0 - q.S));
     };
+
+    // The first unit's Q and first tile; a stream-K segment loads the next
+    // segment's during its own last tile (head dims up to 128: at 256 the
+    // extra registers would spill), else at the segment's start.
+    constexpr bool kPrefetchNext = kStreamK;
+    load_q(wu);
+    {
+        const KvView<uint16_t> kv0(a.kv, wu.sq, wu.h);
+        fetch_tile(kv0, wu.sq, wu.k_begin);
+    }
+    for (bool first_seg = true;; first_seg = false) {
+    const Seq &sq = wu.sq;
+    const int h = wu.h, rb = wu.rb, k_begin = wu.k_begin, k_end = wu.k_end;
+    const int rows = sq.P * a.G;
+    const int r = rb * ROWS + wave * 32 + l32;     // this lane's query row
+    const bool active = rb * ROWS + wave * 32 < rows;
+    const bool qvalid = r < rows;
+    const int qtok = sq.q0 + (qvalid ? r / a.G : 0);
+    const int qhead = h * a.G + (qvalid ? r % a.G : 0);
+    const KvView<uint16_t> kv(a.kv, sq, h);
+    if (!kPrefetchNext && !first_seg) {
+        load_q(wu);
+        fetch_tile(kv, sq, k_begin);
+    }
+    uint64_t mw0 = 0, mw1 = 0;
+    if (qvalid && k_end > sq.S) {
+        const uint64_t *mp = a.mask + (int64_t)qtok * a.mask_words;
+        mw0 = mp[0];
+        if (a.mask_words > 1) mw1 = mp[1];
+    }
+
+    floatx16 o[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db] = floatx16{};
+    float m = -INFINITY, msafe = 0.f, lsum = 0.f;
+    const float c = a.scale_log2;
+
+    // ---- key tiles, each covering keys [t0, t0 + valid), valid <= BN (the
+    // rest of the tile is masked).  The split's prefix keys [k_begin, pre_end)
+    // and pack keys [pk_begin, k_end) are tiled separately: in the store
+    // layout every tile then reads one source, and both layouts add up the
+    // same keys in the same order.
+    const int pre_end = min(k_end, sq.S);
+    const int n_pre = k_begin < pre_end ? (pre_end - k_begin + BN - 1) / BN : 0;
+    const int pk_begin = max(k_begin, sq.S);
+    const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
+    const int ntiles = n_pre + n_pack;
+    auto tile_t0 = [&](int t) __attribute__((always_inline)) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
+    auto tile_valid = [&](int t) __attribute__((always_inline)) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
+    auto fetch = [&](int t) __attribute__((always_inline)) { fetch_tile(kv, sq, tile_t0(t)); };
     // ---- register -> LDS: K as is; V as 8x8 transposed blocks
     auto publish = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -635,17 +856,21 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         }
     };
 
+    // the previous segment's epilogue (its reads of epi) and LDS tiles retire
+    if (!first_seg) __syncthreads();
     if (tid == 0) {
         epi.out = a.out;
         epi.lse = a.lse;
         epi.part_o = a.part_o;
         epi.part_lse = a.part_lse;
+        epi.sk_lse = a.sk_lse;
         epi.status = a.status;
         epi.o_tok = a.o_tok;
         epi.o_head = a.o_head;
-        epi.part_rows = a.part_rows;
-        epi.prow0 = sq.part_off + (int64_t)split * sq.P - sq.q0;
-        epi.ns = sq.ns;
+        epi.part_rows = wu.slot >= 0 ? (int64_t)2 * a.sk_wgs * ROWS : a.part_rows;
+        epi.prow0 = wu.prow0;
+        epi.slot = wu.slot;
+        epi.final_out = wu.final_out;
         epi.Hq = a.Hq;
     }
     __syncthreads();
@@ -757,8 +982,52 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 1);
     };
 
-    // the next tile's loads are in flight during the current tile's MFMA work
-    if (ntiles > 0) fetch(0);
+    // The next tile's loads are in flight during the current tile's MFMA
+    // work.  During a stream-K segment's last tile, the next segment's first
+    // tile and (once this tile's QK product is issued) its Q are loaded.
+    // (The last tile is peeled off the loop, so that the next segment's
+    // values live only there.)
+    Unit nxt;
+    bool has_next = false;
+    if constexpr (kPrefetchNext) {
+    for (int t = 0; t + 1 < ntiles; ++t) {
+        const int buf = t % NBUF;
+        publish(buf);
+        __syncthreads();
+        fetch(t + 1);
+        if (!active) continue;
+        floatx16 s[2];
+        vec8 pb[2][2];
+        qk(buf, s);
+        softmax(t, s, pb);
+        pv(buf, pb);
+    }
+    if (ntiles > 0) {
+        const int t = ntiles - 1;
+        const int buf = t % NBUF;
+        publish(buf);
+        __syncthreads();
+        if (kStreamK && cur.sk) {
+            has_next = sk_next_segment(a, cur, nxt, skr);
+            if (kPrefetchNext && has_next) {
+                const KvView<uint16_t> kvn(a.kv, nxt.sq, nxt.h);
+                fetch_tile(kvn, nxt.sq, nxt.k_begin);
+            }
+        }
+        if (active) {
+            floatx16 s[2];
+            vec8 pb[2][2];
+            qk(buf, s);
+            softmax(t, s, pb);
+            pv(buf, pb);
+        }
+        // the next segment's Q: its latency overlaps this segment's epilogue
+        if (kPrefetchNext && has_next) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_q(nxt);
+        }
+    }
+    } else {
     for (int t = 0; t < ntiles; ++t) {
         const int buf = t % NBUF;
         publish(buf);
@@ -771,44 +1040,52 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         softmax(t, s, pb);
         pv(buf, pb);
     }
+    }
 
-    if (!active) return;
     // ---- epilogue: normalise, write the output or the split partial.
     // O^T element e of lane (l32, g) in block db is d = 32*db + 8*(e/4) + 4*g + e%4.
-    const float ltot = lsum + partner32(lsum);
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
-    if (!qvalid) return;
-    const EpiArgs e = epi;
-    if (e.ns == 1) {
-        uint16_t *op = static_cast<uint16_t *>(e.out) + (int64_t)qtok * e.o_tok + (int64_t)qhead * e.o_head;
+    if (active) {
+        const float ltot = lsum + partner32(lsum);
+        const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+        const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
+        const EpiArgs e = epi;
+        if (qvalid && e.final_out) {
+            uint16_t *op = static_cast<uint16_t *>(e.out) + (int64_t)qtok * e.o_tok + (int64_t)qhead * e.o_head;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int d = db * 32 + 8 * r4 + 4 * g;
-                const u32x2 w = {E::pack2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv),
-                                 E::pack2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv)};
-                *reinterpret_cast<u32x2 *>(op + d) = w;
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = db * 32 + 8 * r4 + 4 * g;
+                    const u32x2 w = {E::pack2(o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv),
+                                     E::pack2(o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv)};
+                    *reinterpret_cast<u32x2 *>(op + d) = w;
+                }
+            if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
+        } else if (qvalid) {
+            // static split: row (token, head) of the partial rows; stream-K:
+            // row wave * 32 + l32 of the workgroup's slot
+            const int64_t prow = e.slot >= 0 ? (int64_t)e.slot * ROWS + wave * 32 + l32 : e.prow0 + qtok;
+            if (prow >= e.part_rows) {
+                raise_flag(e.status, CAST_FLAG_BAD_OFFSETS);
+            } else {
+                const int64_t orow = e.slot >= 0 ? prow : prow * e.Hq + qhead;
+                float *pp = e.part_o + orow * D;
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const int d = db * 32 + 8 * r4 + 4 * g;
+                        const floatx4 w = {o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
+                                           o[db][4 * r4 + 3] * inv};
+                        *reinterpret_cast<floatx4 *>(pp + d) = w;
+                    }
+                if (g == 0) (e.slot >= 0 ? e.sk_lse : e.part_lse)[orow] = lse2;
             }
-        if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
-    } else {
-        const int64_t prow = e.prow0 + qtok;
-        if (prow >= e.part_rows) {
-            raise_flag(e.status, CAST_FLAG_BAD_OFFSETS);
-            return;
         }
-        float *pp = e.part_o + (prow * e.Hq + qhead) * D;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int d = db * 32 + 8 * r4 + 4 * g;
-                const floatx4 w = {o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
-                                   o[db][4 * r4 + 3] * inv};
-                *reinterpret_cast<floatx4 *>(pp + d) = w;
-            }
-        if (g == 0) e.part_lse[prow * e.Hq + qhead] = lse2;
+    }
+    if constexpr (kStreamK && !kPrefetchNext) has_next = cur.sk && sk_next_segment(a, cur, nxt, skr);
+    if (!has_next) break;
+    wu = nxt;
     }
 }
 // --------------------------------------------------------------------------
@@ -832,7 +1109,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 // 4-wave head_dim-128 instance (1): its threads each stage twice the 8-wave
 // instance's share of a tile, and its 135 KB of LDS leave room for one
 // workgroup (one wave per SIMD) per CU anyway.
-template <int D, int WAVES, bool STORE, int WPE = 2>
+template <int D, int WAVES, bool STORE, int WPE = 2, bool SKI = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void tree_attn_f32_kernel(AttnArgs a) {
     constexpr int NT = WAVES * 64;
@@ -850,18 +1127,19 @@ void tree_attn_f32_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float Ks[2][BN * KPAD];
     __shared__ __attribute__((aligned(16))) float Vs[2][BN * KPAD];
     __shared__ EpiArgs epi;
+    __shared__ SkReq skr[SKI ? 64 : 1];
 
-    Seq sq;
-    int rb, split, h;
-    if (!locate_item(a, sq, h, split, rb)) return;
-    const int k_begin = split * sq.split_len;
-    const int k_end = min(sq.T, k_begin + sq.split_len);
-
+    Unit wu;
+    WorkCursor cur;
+    if (!first_unit<SKI>(a, cur, wu, skr)) return;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const int g = lane >> 5;
     const int l32 = lane & 31;
+    do {
+    const Seq &sq = wu.sq;
+    const int h = wu.h, rb = wu.rb, k_begin = wu.k_begin, k_end = wu.k_end;
     const int rows = sq.P * a.G;
     const int r = rb * ROWS + wave * 32 + l32;
     const bool active = rb * ROWS + wave * 32 < rows;
@@ -971,12 +1249,14 @@ void tree_attn_f32_kernel(AttnArgs a) {
         epi.lse = a.lse;
         epi.part_o = a.part_o;
         epi.part_lse = a.part_lse;
+        epi.sk_lse = a.sk_lse;
         epi.status = a.status;
         epi.o_tok = a.o_tok;
         epi.o_head = a.o_head;
-        epi.part_rows = a.part_rows;
-        epi.prow0 = sq.part_off + (int64_t)split * sq.P - sq.q0;
-        epi.ns = sq.ns;
+        epi.part_rows = wu.slot >= 0 ? (int64_t)2 * a.sk_wgs * ROWS : a.part_rows;
+        epi.prow0 = wu.prow0;
+        epi.slot = wu.slot;
+        epi.final_out = wu.final_out;
         epi.Hq = a.Hq;
     }
     __syncthreads();
@@ -1055,45 +1335,153 @@ void tree_attn_f32_kernel(AttnArgs a) {
             }
     }
 
-    if (!active) return;
-    const float ltot = lsum + partner32(lsum);
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
-    if (!qvalid) return;
-    const EpiArgs e = epi;
-    float *dst;
-    if (e.ns == 1) {
-        dst = static_cast<float *>(e.out) + (int64_t)qtok * e.o_tok + (int64_t)qhead * e.o_head;
-        if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
-    } else {
-        const int64_t prow = e.prow0 + qtok;
-        if (prow >= e.part_rows) {
-            raise_flag(e.status, CAST_FLAG_BAD_OFFSETS);
-            return;
+    if (active && qvalid) {
+        const float ltot = lsum + partner32(lsum);
+        const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+        const float lse2 = ltot > 0.f ? msafe + log2f(ltot) : -INFINITY;
+        const EpiArgs e = epi;
+        float *dst = nullptr;
+        if (e.final_out) {
+            dst = static_cast<float *>(e.out) + (int64_t)qtok * e.o_tok + (int64_t)qhead * e.o_head;
+            if (e.lse && g == 0) e.lse[(int64_t)qtok * e.Hq + qhead] = lse2 * kLn2;
+        } else {
+            // static split: row (token, head) of the partial rows; stream-K:
+            // row wave * 32 + l32 of the workgroup's slot
+            const int64_t prow = e.slot >= 0 ? (int64_t)e.slot * ROWS + wave * 32 + l32 : e.prow0 + qtok;
+            if (prow >= e.part_rows) {
+                raise_flag(e.status, CAST_FLAG_BAD_OFFSETS);
+            } else {
+                const int64_t orow = e.slot >= 0 ? prow : prow * e.Hq + qhead;
+                dst = e.part_o + orow * D;
+                if (g == 0) (e.slot >= 0 ? e.sk_lse : e.part_lse)[orow] = lse2;
+            }
         }
-        dst = e.part_o + (prow * e.Hq + qhead) * D;
-        if (g == 0) e.part_lse[prow * e.Hq + qhead] = lse2;
+        if (dst) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int d = db * 32 + 8 * r4 + 4 * g;
+                    const floatx4 w = {o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
+                                       o[db][4 * r4 + 3] * inv};
+                    *reinterpret_cast<floatx4 *>(dst + d) = w;
+                }
+        }
     }
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            const int d = db * 32 + 8 * r4 + 4 * g;
-            const floatx4 w = {o[db][4 * r4] * inv, o[db][4 * r4 + 1] * inv, o[db][4 * r4 + 2] * inv,
-                               o[db][4 * r4 + 3] * inv};
-            *reinterpret_cast<floatx4 *>(dst + d) = w;
-        }
+    } while (SKI && next_unit(a, cur, wu, skr));
 }
 
 // --------------------------------------------------------------------------
 // Split-K combine: one workgroup per packed token, all query heads.
 // --------------------------------------------------------------------------
-// One workgroup per (packed token, group of query heads): a.comb_groups
-// groups of ceil(Hq / comb_groups) heads, each thread one 4-wide chunk of a
-// head's output at a time.
-template <typename OutT, int D, typename E>   // E: the 16-bit format when OutT is 2 bytes
+// The stream-K merge of token tok (index i of request sq) for query heads
+// [h0, hend): each head's unit (KV head, row block) sits in super-group
+// s = unit / 2, lane-steps [g0, g0 + tiles) of the lane line, which lanes
+// g0 / L .. (g0 + tiles - 1) / L cover; one lane means the attention kernel
+// wrote the output itself.  Otherwise piece l is member (unit % 2) of lane l:
+// slot 2x + 1 for the first lane when the super-group starts inside it (the
+// lane's last segment), slot 2x for the others (their first segment).  The
+// pieces' lse and weights go through LDS, then every 4-wide chunk of the
+// heads' outputs merges its pieces.
+// The LDS of the combine kernel: per (head, split) lse then weights, and
+// per head max and sum; the stream-K instance adds each piece's partial row
+// and each head's piece count.
+struct CombineLds {
+    float wgt[kCombineLdsHeads * kCombineLdsSplits];
+    float hm[kCombineLdsHeads], hl[kCombineLdsHeads];
+};
+struct CombineLdsSk : CombineLds {
+    int prow[kCombineLdsHeads * kSkMaxPieces];
+    int hn[kCombineLdsHeads];
+};
+
+template <typename OutT, int D, typename E>
+__device__ void combine_stream_k(const AttnArgs &a, const SkPlan &pl, const Seq &sq, int i, int tok, int h0,
+                                 int hend, int base, int tiles, CombineLdsSk &sm) {
+    constexpr int C = D / 4;
+    constexpr int NP = kSkMaxPieces;
+    static_assert(kSkMaxPieces <= kCombineLdsSplits, "pieces share the split table");
+    const int nh = hend - h0;   // <= kCombineLdsHeads (the host sizes the head groups)
+    const int rows_wg = a.rows_wg, G = a.G, nx = a.xcds, L = pl.L;
+    // one thread per head: its unit, the lanes its super-group spans and
+    // the partial row of every piece; the pieces' lse into LDS
+    if (threadIdx.x < nh) {
+        const int hh = threadIdx.x, hq = h0 + hh;
+        const int r = i * G + hq % G;
+        const int unit = (hq / G) * sq.rb + r / rows_wg;
+        const int64_t g0 = (int64_t)base + (int64_t)(unit >> 1) * tiles;
+        const int l0 = (int)(g0 / L), l1 = (int)((g0 + tiles - 1) / L);
+        const int n = l1 > l0 ? l1 - l0 + 1 : 0;
+        sm.hn[hh] = n;
+        float M = -INFINITY;
+        for (int p0 = 0; p0 < n; p0 += kCombineUnroll) {
+            float l[kCombineUnroll];
+#pragma unroll
+            for (int k = 0; k < kCombineUnroll; ++k) {
+                const int piece = p0 + k;
+                const int x = sk_wg_of(l0 + piece, unit & 1, nx);
+                const int slot = 2 * x + (piece == 0 && g0 != (int64_t)l0 * L ? 1 : 0);
+                const int row = slot * rows_wg + r % rows_wg;
+                if (piece < n) sm.prow[hh * NP + piece] = row;
+                l[k] = piece < n ? a.sk_lse[row] : -INFINITY;
+            }
+#pragma unroll
+            for (int k = 0; k < kCombineUnroll; ++k) {
+                if (p0 + k < n) sm.wgt[hh * NP + p0 + k] = l[k];
+                M = fmaxf(M, l[k]);
+            }
+        }
+        float S = 0.f;
+        for (int piece = 0; piece < n; ++piece) {
+            const float w = M == -INFINITY ? 0.f : exp2f(sm.wgt[hh * NP + piece] - M);
+            sm.wgt[hh * NP + piece] = w;
+            S += w;
+        }
+        sm.hm[hh] = M;
+        sm.hl[hh] = S;
+    }
+    __syncthreads();
+    // every 4-wide chunk of the heads' outputs: all its pieces' loads in
+    // flight at once (up to kCombineUnroll), then the weighted sum
+    for (int c = threadIdx.x; c < nh * C; c += blockDim.x) {
+        const int hh = c / C, d4 = c % C;
+        const int n = sm.hn[hh];
+        if (n == 0) continue;
+        const float M = sm.hm[hh], S = sm.hl[hh];
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (M != -INFINITY) {
+            const int *rw = sm.prow + hh * NP;
+            const float *w = sm.wgt + hh * NP;
+            for (int s0 = 0; s0 < n; s0 += kCombineUnroll) {
+                floatx4 x[kCombineUnroll];
+#pragma unroll
+                for (int k = 0; k < kCombineUnroll; ++k)
+                    x[k] = s0 + k < n ? *reinterpret_cast<const floatx4 *>(a.part_o + (int64_t)rw[s0 + k] * D + d4 * 4)
+                                      : floatx4{};
+#pragma unroll
+                for (int k = 0; k < kCombineUnroll; ++k)
+                    if (s0 + k < n) acc += w[s0 + k] * x[k];
+            }
+            acc *= 1.f / S;
+        }
+        const int hq = h0 + hh;
+        OutT *op = static_cast<OutT *>(a.out) + (int64_t)tok * a.o_tok + (int64_t)hq * a.o_head + d4 * 4;
+        if constexpr (sizeof(OutT) == 2) {
+            const u32x2 w2 = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
+            *reinterpret_cast<u32x2 *>(op) = w2;
+        } else {
+            *reinterpret_cast<floatx4 *>(op) = acc;
+        }
+        if (a.lse && d4 == 0)
+            a.lse[(int64_t)tok * a.Hq + hq] = M == -INFINITY ? -INFINITY : (M + log2f(S)) * kLn2;
+    }
+}
+
+// E: the 16-bit format when OutT is 2 bytes; SKI: merges stream-K pieces
+template <typename OutT, int D, typename E, bool SKI = false>
 __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
     constexpr int C = D / 4;
+    __shared__ typename std::conditional<SKI, CombineLdsSk, CombineLds>::type sm;
     const int groups = a.comb_groups;
     const int tok = blockIdx.x / groups;
     const int hpg = (a.Hq + groups - 1) / groups;
@@ -1112,12 +1500,21 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
         if (rejected(tot)) return;
         const int pp = ok && t.ns > 1 ? sat32((int64_t)t.ns * t.P) : 0;
         const int p_excl = wave_scan(pp) - pp;
+        int base = 0, cost = 0, tiles = 0;
+        const SkPlan pl = SKI ? sk_plan(a, t, ok, base, cost, tiles) : SkPlan{false, 0, 0};
         const uint64_t hit = __ballot(ok && tok >= t.q0 && tok < t.q0 + t.P);
         if (!hit) return;
         const int src = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hit));
         sq = shfl_seq(t, src);
         sq.part_off = bcast(p_excl, src);
         i = tok - sq.q0;
+        if constexpr (SKI) {
+            if (pl.use) {
+                combine_stream_k<OutT, D, E>(a, pl, sq, i, tok, h0, min(a.Hq, h0 + hpg), bcast(base, src),
+                                             bcast(tiles, src), sm);
+                return;
+            }
+        }
     } else {
         if (rejected(batch_totals(a))) return;
         if (!find_request(a, tok, true, sq, i)) return;
@@ -1187,8 +1584,8 @@ __global__ __launch_bounds__(256) void tree_attn_combine_kernel(AttnArgs a) {
         // trip) and each head's max, sum and weights computed once, in LDS;
         // then each chunk loads its ns partials kCombineUnroll at a time.
         // Same operations in the same order as the loop below: same bits.
-        __shared__ float wgt[kCombineLdsHeads * kCombineLdsSplits];
-        __shared__ float hm[kCombineLdsHeads], hl[kCombineLdsHeads];
+        float *wgt = sm.wgt;
+        float *hm = sm.hm, *hl = sm.hl;
         const float *lp0 = a.part_lse + (sq.part_off + i) * a.Hq + h0;
         for (int t = threadIdx.x; t < nh * ns; t += 256) wgt[t] = lp0[(t / ns) + (t % ns) * lstride];
         __syncthreads();
@@ -1432,6 +1829,105 @@ static int64_t part_rows_bound(int32_t total_q, int32_t total_kv, int32_t chunk)
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// kv_split value that asks for the stream-K schedule.
+constexpr int32_t kSplitStreamK = -2;
+
+// The MFMA attention kernel instance of a call and its block size.
+struct AttnKernel {
+    const void *fn;
+    int threads;
+};
+template <int DD, int W, int WPE, bool SKI>
+static AttnKernel mfma_instance(bool f16, bool store) {
+    const void *fn =
+        f16 ? (store ? reinterpret_cast<const void *>(&tree_attn_mfma_kernel<DD, W, true, Fp16, WPE, SKI>)
+                     : reinterpret_cast<const void *>(&tree_attn_mfma_kernel<DD, W, false, Fp16, WPE, SKI>))
+            : (store ? reinterpret_cast<const void *>(&tree_attn_mfma_kernel<DD, W, true, Bf16, WPE, SKI>)
+                     : reinterpret_cast<const void *>(&tree_attn_mfma_kernel<DD, W, false, Bf16, WPE, SKI>));
+    return {fn, W * 64};
+}
+template <int DD, int W, int WPE, bool SKI>
+static AttnKernel f32_instance(bool store) {
+    const void *fn = store ? reinterpret_cast<const void *>(&tree_attn_f32_kernel<DD, W, true, WPE, SKI>)
+                           : reinterpret_cast<const void *>(&tree_attn_f32_kernel<DD, W, false, WPE, SKI>);
+    return {fn, W * 64};
+}
+template <bool SKI>
+static AttnKernel attn_kernel_of(int32_t dtype, int32_t D, int waves, bool store) {
+    if (dtype == CAST_FP32) {
+        if (D == 128) return waves == 4 ? f32_instance<128, 4, 1, SKI>(store) : f32_instance<128, 8, 2, SKI>(store);
+        return waves == 4 ? f32_instance<64, 4, 2, SKI>(store) : f32_instance<64, 8, 2, SKI>(store);
+    }
+    const bool f16 = dtype == CAST_FP16;
+    if (D == 128) {
+        if (waves == 2) return mfma_instance<128, 2, 1, SKI>(f16, store);
+        return waves == 4 ? mfma_instance<128, 4, 2, SKI>(f16, store) : mfma_instance<128, 8, 2, SKI>(f16, store);
+    }
+    if (waves == 2) return mfma_instance<64, 2, 2, SKI>(f16, store);
+    return waves == 4 ? mfma_instance<64, 4, 2, SKI>(f16, store) : mfma_instance<64, 8, 2, SKI>(f16, store);
+}
+// Head dims 64 and 128 run 2, 4 or 8 waves (bf16 / fp16) or 4 or 8 (fp32);
+// head dim 256 runs 4 (bf16 / fp16, static schedule only).  WPE (waves per
+// SIMD of the register budget) as the kernels' comments give it; sk picks
+// the stream-K instance.
+static AttnKernel attn_kernel(int32_t dtype, int32_t D, int waves, bool store, bool sk) {
+    if (D == 256) return mfma_instance<256, 4, 1, false>(dtype == CAST_FP16, store);
+    return sk ? attn_kernel_of<true>(dtype, D, waves, store) : attn_kernel_of<false>(dtype, D, waves, store);
+}
+
+// Workgroups of kernel k resident on one CU of the current device (1 where
+// no device is visible), looked up once per (device, kernel).
+static int resident_per_cu(const AttnKernel &k) {
+    struct Entry {
+        int dev;
+        const void *fn;
+        int n;
+    };
+    static std::mutex mu;
+    static Entry cache[256];
+    static int used = 0;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+        if (cache[i].dev == dev && cache[i].fn == k.fn) return cache[i].n;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k.fn, k.threads, 0) != hipSuccess || n < 1) n = 1;
+    if (used < 256) cache[used++] = Entry{dev, k.fn, n};
+    return n;
+}
+
+// Stream-K figures of a call: whether the caller asked for the schedule
+// (kv_split = CAST_SPLIT_STREAM, batches of up to 64 requests, head dims 64
+// and 128) and its workgroup count - every CU's resident workgroups of the
+// concat-layout stream-K instance (the store-layout instance only differs
+// in its addressing), a multiple of two per XCD.
+struct SkHost {
+    int mode, wgs, rows_wg;
+};
+static SkHost sk_host(int32_t batch, int32_t total_q, int32_t G, int32_t D, int32_t dtype, int32_t kv_split,
+                      int32_t chunk) {
+    SkHost h{0, 0, 0};
+    if (!mfma_path(dtype, D) || D > 128 || batch <= 0 || batch > 64) return h;
+    if (kv_split != kSplitStreamK) return h;
+    h.mode = 1;
+    const int waves = waves_for(total_q, G, dtype, D);
+    const Topology topo = device_topology();
+    const int per = resident_per_cu(attn_kernel(dtype, D, waves, false, true));
+    const int step = 2 * topo.xcds;
+    h.wgs = (topo.cus * per) / step * step;
+    h.rows_wg = waves * 32;
+    if (h.wgs < step) h.mode = 0;
+    return h;
+}
+
+// Bytes of stream-K partials: O [2 * wgs][rows_wg][D] then lse [2 * wgs][rows_wg].
+static size_t sk_bytes(const SkHost &h, int32_t D) {
+    if (!h.mode) return 0;
+    const size_t rows = (size_t)2 * h.wgs * h.rows_wg;
+    return align256(rows * D * sizeof(float)) + align256(rows * sizeof(float));
+}
+
 }  // namespace cast
 
 using namespace cast;
@@ -1450,10 +1946,15 @@ extern "C" size_t cast_tree_attn_workspace_size(int32_t batch, int32_t total_q, 
     if (batch <= 0 || total_q <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return 0;
     const int32_t chunk = resolve_chunk(batch, total_q, total_kv, num_q_heads, num_kv_heads, head_dim,
                                         dtype, kv_split);
-    if (chunk == kNoSplit) return 0;
-    const int64_t rows = part_rows_bound(total_q, total_kv, chunk);
-    return align256((size_t)rows * num_q_heads * head_dim * sizeof(float)) +
-           align256((size_t)rows * num_q_heads * sizeof(float));
+    size_t bytes = 0;
+    if (chunk != kNoSplit) {
+        const int64_t rows = part_rows_bound(total_q, total_kv, chunk);
+        bytes = align256((size_t)rows * num_q_heads * head_dim * sizeof(float)) +
+                align256((size_t)rows * num_q_heads * sizeof(float));
+    }
+    const SkHost sk = sk_host(batch, total_q, num_q_heads / num_kv_heads, head_dim, dtype, kv_split, chunk);
+    const size_t skb = sk_bytes(sk, head_dim);
+    return skb > bytes ? skb : bytes;
 }
 
 enum { kStageAttn = 1, kStageCombine = 2 };
@@ -1551,19 +2052,29 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     const int waves = waves_for(total_q, a.G, dtype, head_dim);
     a.rows_wg = waves * 32;
     a.chunk = resolve_chunk(batch, total_q, total_kv, num_q_heads, num_kv_heads, head_dim, dtype, kv_split);
-    if (a.chunk != kNoSplit) {
+    const SkHost sk = sk_host(batch, total_q, a.G, head_dim, dtype, kv_split, a.chunk);
+    a.sk_mode = sk.mode;
+    a.sk_wgs = sk.mode ? sk.wgs : 0;
+    a.sk_min_tiles = kMinChunk / 64;
+    if (a.chunk != kNoSplit || sk.mode) {
         const size_t need = cast_tree_attn_workspace_size(batch, total_q, total_kv, num_q_heads, num_kv_heads,
                                                           head_dim, dtype, kv_split);
         if (!workspace || workspace_bytes < need) return CAST_ERR_WORKSPACE;
         if (reinterpret_cast<uintptr_t>(workspace) & 255) return CAST_ERR_ALIGNMENT;
-        a.part_rows = part_rows_bound(total_q, total_kv, a.chunk);
         a.part_o = static_cast<float *>(workspace);
-        a.part_lse = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                               align256((size_t)a.part_rows * num_q_heads * head_dim * sizeof(float)));
+        if (a.chunk != kNoSplit) {
+            a.part_rows = part_rows_bound(total_q, total_kv, a.chunk);
+            a.part_lse = reinterpret_cast<float *>(
+                static_cast<char *>(workspace) + align256((size_t)a.part_rows * num_q_heads * head_dim * sizeof(float)));
+        }
+        if (sk.mode)
+            a.sk_lse = reinterpret_cast<float *>(
+                static_cast<char *>(workspace) + align256((size_t)2 * sk.wgs * sk.rows_wg * head_dim * sizeof(float)));
     }
     // Grid bound without reading device metadata: every request has at most
     // min(total_q, 128) tokens, so row blocks per (request, head, split) are
-    // bounded, and splits sum to at most total_kv / chunk + batch.
+    // bounded, and splits sum to at most total_kv / chunk + batch.  The
+    // stream-K schedule needs sk_wgs workgroups; the device picks one.
     const int64_t pmax = total_q < kMaxPack ? total_q : kMaxPack;
     const int64_t rbmax = (pmax * a.G + a.rows_wg - 1) / a.rows_wg;
     const int64_t nsplit = a.chunk == kNoSplit ? batch : ((int64_t)total_kv + a.chunk - 1) / a.chunk + batch;
@@ -1571,64 +2082,41 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     a.xcds = device_topology().xcds;
     items = batch <= 64 ? sorted_slots((int64_t)num_kv_heads * nsplit, rbmax, a.xcds)
                         : (items + a.xcds - 1) / a.xcds * a.xcds;
-    const unsigned grid = (unsigned)items;
-#define CAST_LAUNCH_E(DD, W, E, WPE)                                                \
-    (kv.store ? tree_attn_mfma_kernel<DD, W, true, E, WPE><<<grid, W * 64, 0, st>>>(a) \
-              : tree_attn_mfma_kernel<DD, W, false, E, WPE><<<grid, W * 64, 0, st>>>(a))
-#define CAST_LAUNCH(DD, W, WPE) (f16 ? CAST_LAUNCH_E(DD, W, Fp16, WPE) : CAST_LAUNCH_E(DD, W, Bf16, WPE))
-#define CAST_LAUNCH_WIDE_E(W, E)                                                       \
-    (kv.store ? tree_attn_mfma_kernel<256, W, true, E, 1><<<grid, W * 64, 0, st>>>(a) \
-              : tree_attn_mfma_kernel<256, W, false, E, 1><<<grid, W * 64, 0, st>>>(a))
-#define CAST_LAUNCH_WIDE(W) (f16 ? CAST_LAUNCH_WIDE_E(W, Fp16) : CAST_LAUNCH_WIDE_E(W, Bf16))
-#define CAST_LAUNCH_F32(DD, W, WPE)                                                \
-    (kv.store ? tree_attn_f32_kernel<DD, W, true, WPE><<<grid, W * 64, 0, st>>>(a) \
-              : tree_attn_f32_kernel<DD, W, false, WPE><<<grid, W * 64, 0, st>>>(a))
-    const bool f16 = dtype == CAST_FP16;
-    if (!(stages & kStageAttn)) {
-    } else if (dtype == CAST_FP32) {
-        if (head_dim == 128) {
-            if (waves == 4) CAST_LAUNCH_F32(128, 4, 1);
-            else CAST_LAUNCH_F32(128, 8, 2);
-        } else {
-            if (waves == 4) CAST_LAUNCH_F32(64, 4, 2);
-            else CAST_LAUNCH_F32(64, 8, 2);
-        }
-    } else if (head_dim == 256) {
-        CAST_LAUNCH_WIDE(4);
-    } else if (head_dim == 128) {
-        if (waves == 2) CAST_LAUNCH(128, 2, 1);
-        else if (waves == 4) CAST_LAUNCH(128, 4, 2);
-        else CAST_LAUNCH(128, 8, 2);
-    } else {
-        if (waves == 2) CAST_LAUNCH(64, 2, 2);
-        else if (waves == 4) CAST_LAUNCH(64, 4, 2);
-        else CAST_LAUNCH(64, 8, 2);
+    if (a.sk_mode && items < a.sk_wgs) items = a.sk_wgs;
+    if (items > 0x7fffffff) return CAST_ERR_SHAPE;
+    if (stages & kStageAttn) {
+        const AttnKernel k = attn_kernel(dtype, head_dim, waves, kv.store != 0, a.sk_mode != 0);
+        void *args[] = {&a};
+        if (hipLaunchKernel(k.fn, dim3((unsigned)items), dim3(k.threads), args, 0, st) != hipSuccess)
+            return CAST_ERR_HIP;
     }
-#undef CAST_LAUNCH
-#undef CAST_LAUNCH_E
-#undef CAST_LAUNCH_WIDE
-#undef CAST_LAUNCH_WIDE_E
-#undef CAST_LAUNCH_F32
     if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
-    if (a.chunk != kNoSplit && (stages & kStageCombine)) {
+    if ((a.chunk != kNoSplit || a.sk_mode) && (stages & kStageCombine)) {
         // about 1536 workgroups (6 per CU), each with up to 256 output chunks
+        // of at most kCombineLdsHeads heads
         const int64_t max_groups = ((int64_t)num_q_heads * (head_dim / 4) + 255) / 256;
+        const int64_t min_groups = (num_q_heads + kCombineLdsHeads - 1) / kCombineLdsHeads;
         int64_t g = 1536 / total_q;
         g = g < 1 ? 1 : (g > max_groups ? max_groups : g);
+        g = g < min_groups ? min_groups : g;
         a.comb_groups = (int32_t)g;
         const unsigned cg = (unsigned)(total_q * g);
+#define CAST_COMBINE(OT, DD, E)                                                         \
+    (a.sk_mode ? tree_attn_combine_kernel<OT, DD, E, true><<<cg, 256, 0, st>>>(a) \
+               : tree_attn_combine_kernel<OT, DD, E, false><<<cg, 256, 0, st>>>(a))
         if (dtype == CAST_FP32) {
-            if (head_dim == 128) tree_attn_combine_kernel<float, 128, Bf16><<<cg, 256, 0, st>>>(a);
-            else tree_attn_combine_kernel<float, 64, Bf16><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 128) CAST_COMBINE(float, 128, Bf16);
+            else CAST_COMBINE(float, 64, Bf16);
         } else if (dtype == CAST_FP16) {
-            if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Fp16><<<cg, 256, 0, st>>>(a);
-            else if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Fp16><<<cg, 256, 0, st>>>(a);
-            else tree_attn_combine_kernel<uint16_t, 64, Fp16><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Fp16, false><<<cg, 256, 0, st>>>(a);
+            else if (head_dim == 128) CAST_COMBINE(uint16_t, 128, Fp16);
+            else CAST_COMBINE(uint16_t, 64, Fp16);
         } else {
-            if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Bf16><<<cg, 256, 0, st>>>(a);
-            else if (head_dim == 128) tree_attn_combine_kernel<uint16_t, 128, Bf16><<<cg, 256, 0, st>>>(a);
-            else tree_attn_combine_kernel<uint16_t, 64, Bf16><<<cg, 256, 0, st>>>(a);
+            if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Bf16, false><<<cg, 256, 0, st>>>(a);
+            else if (head_dim == 128) CAST_COMBINE(uint16_t, 128, Bf16);
+            else CAST_COMBINE(uint16_t, 64, Bf16);
         }
+#undef CAST_COMBINE
         if (hipGetLastError() != hipSuccess) return CAST_ERR_HIP;
     }
     return CAST_OK;
@@ -1711,7 +2199,7 @@ extern "C" int cast_tree_attn_store_fwd(const void *q, const void *k_store, cons
 // the array and race.
 // --------------------------------------------------------------------------
 namespace cast {
-constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr size_t kScratchBytes = (size_t)72 << 20;
 constexpr int kMaxDevices = 64;
 }  // namespace cast
 

@@ -98,7 +98,18 @@ int cast_tree_bitmask(const int32_t *parent, const int32_t *cu_q, int32_t batch,
  *          takes any power of two)
  *   sm_scale  > 0 (the Python layer substitutes 1/sqrt(D) for None)
  *   kv_split  keys per split-K chunk (multiple of 64); 0 lets the library
- *             choose from the shapes; a negative value disables split-K
+ *             choose; CAST_SPLIT_STREAM (-2) asks for the stream-K schedule;
+ *             any other negative value disables split-K.  With 0 the library
+ *             cuts long prefixes into equal splits, and for batches of up to
+ *             64 requests whose splits would leave the GPU unbalanced
+ *             (ragged prefixes), the kernels take the stream-K schedule
+ *             instead: pairs of workgroups on one XCD get equal ranges of
+ *             key tiles over all (request, KV head, row block) units, and a
+ *             combine merges the pieces of units cut between workgroups.
+ *             That choice is made on the device from the metadata.  The
+ *             static schedule sums each request's keys in an order that only
+ *             depends on batch totals; stream-K's cut points follow the batch
+ *             order.
  *   workspace / workspace_bytes  scratch of at least
  *             cast_tree_attn_workspace_size(...) bytes, 256-byte aligned
  *   status    int32*, nullable device status word
@@ -181,7 +192,7 @@ int cast_tree_attn_store_fwd(const void *q, const void *k_store, const void *v_s
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory during the call: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  The split-K partials go to a static
- * device array of cast_tree_attn_noalloc_limit() bytes (64 MiB), which every
+ * device array of cast_tree_attn_noalloc_limit() bytes (72 MiB), which every
  * GPU the library runs on holds until the process ends.  Calls whose
  * cast_tree_attn_workspace_size(...) exceeds it return
  * CAST_ERR_SCRATCH_LIMIT before any device work (a larger kv_split, or -1,
@@ -202,7 +213,14 @@ int cast_tree_attn_fwd_noalloc(const void *q, const void *k, const void *v, void
 /* Bytes of the static split-K scratch of cast_tree_attn_fwd_noalloc. */
 size_t cast_tree_attn_noalloc_limit(void);
 
-/* Workspace bytes cast_tree_attn_fwd needs for these host-known sizes. */
+/* kv_split value asking for the stream-K schedule (batches of up to 64
+ * requests on the MFMA kernels with head dims 64 and 128; otherwise the
+ * same as -1). */
+#define CAST_SPLIT_STREAM (-2)
+
+/* Workspace bytes cast_tree_attn_fwd needs for these host-known sizes (and
+ * the current device's CU count: the stream-K partials take two slots of
+ * rows_per_workgroup x (head_dim + 1) floats per resident workgroup). */
 size_t cast_tree_attn_workspace_size(int32_t batch, int32_t total_q, int32_t total_kv,
                                      int32_t num_q_heads, int32_t num_kv_heads,
                                      int32_t head_dim, int32_t dtype, int32_t kv_split);

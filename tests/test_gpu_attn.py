@@ -243,9 +243,11 @@ def test_metadata_errors_are_flagged_not_faulted(gpu):
 
 
 def test_request_order_is_irrelevant(gpu):
-    # a full-size property: each request is computed on its own, and the
-    # split plan depends only on batch totals, so reordering the requests of
-    # a packed batch reorders the outputs and LSE bit for bit
+    # a full-size property of the static split schedule: each request is
+    # computed on its own, and the split plan depends only on batch totals,
+    # so reordering the requests of a packed batch reorders the outputs and
+    # LSE bit for bit.  (The stream-K schedule cuts its lanes along the batch
+    # order, so there the bits of a request depend on its neighbours.)
     from cast_amd import varlen_tree_attention
     wl = SC.qwen3_ragged(seed=5)
     print(f"case request-order: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv}", flush=True)
@@ -267,7 +269,7 @@ def test_request_order_is_irrelevant(gpu):
         pre = torch.tensor([int(wl.prefix_len[b]) for b in order], dtype=torch.int32, device=gpu)
         pk = torch.tensor([int(wl.pack_len[b]) for b in order], dtype=torch.int32, device=gpu)
         out, lse = varlen_tree_attention(torch.cat(qs), torch.cat(ks), torch.cat(vs), cq, ck, pre, pk,
-                                         torch.cat(ws), return_lse=True, check=True)
+                                         torch.cat(ws), return_lse=True, check=True, kv_split=1024)
         torch.cuda.synchronize()
         return out, lse, lq
 
@@ -314,3 +316,90 @@ def test_fp32_edges_and_head_dim_64(gpu):
 def test_fp32_large_configs_sampled(gpu):
     for wl, reqs in [(_fp32(SC.qwen3_headline()), [0, 7]), (_fp32(SC.stress_mixed()), [3, 30])]:
         _run_and_check(wl, gpu, requests=reqs, kv_heads=[0, 5], label=wl.name)
+
+
+# ---- the stream-K schedule (kv_split=-2 asks for it; the library also takes
+# it by itself when the static splits are unbalanced)
+
+def _edges(dtype="bf16"):
+    from cast_amd.tree import TreeNode
+    chain = [TreeNode(i, i + 1, i - 1, 0.0) for i in range(127)]
+    star = [TreeNode(i, 1, -1, 0.0) for i in range(127)]
+    return SC._make("edges", [chain, [], star, chain[:5], star[:63]], [0, 77, 1, 4099, 33], SC.QWEN3_8B, dtype, 5,
+                    1 / math.sqrt(128))
+
+
+STREAM_K_CASES = {
+    # B=8, P < 64: one row block per head, two heads per super-group
+    "reference-bf16": lambda: SC.random_parent_batch(seed=0, dtype="bf16"),
+    "reference-fp32": lambda: SC.random_parent_batch(seed=0, dtype="fp32"),
+    "reference-fp16": lambda: SC.random_parent_batch(seed=1, dtype="fp16"),
+    # P up to 128 (two row blocks of one head per super-group), long prefixes
+    "ragged-small": lambda: SC.qwen3_ragged(seed=3, B=4, lo=100, hi=3000),
+    # one KV head (16 row blocks per request), head dim 64
+    "mqa-d64": lambda: SC.random_parent_batch(seed=12, B=3, Hq=32, Hkv=1, D=64, s_lo=50, s_hi=1500, p_lo=1,
+                                               p_hi=129, dtype="bf16", qkv_scale=0.5),
+    # three KV heads with one row block each: the second super-group has one
+    # unit, so one member of its lanes idles there
+    "odd-heads": lambda: SC.random_parent_batch(seed=13, B=5, Hq=12, Hkv=3, D=128, s_lo=50, s_hi=2000, p_lo=1,
+                                                 p_hi=30, dtype="bf16", qkv_scale=0.5),
+    # S = 0, P = 1, 128-token chain and star, S not a multiple of 64
+    "edges": _edges,
+    "head-dim-256": lambda: SC.random_parent_batch(seed=7, B=4, Hq=16, Hkv=8, D=256, s_lo=500, s_hi=4000, p_lo=1,
+                                                    p_hi=129, dtype="bf16", qkv_scale=0.5),
+    "single-p16": lambda: SC.qwen3_single(),
+    "fp32-ragged": lambda: _fp32(SC.qwen3_ragged(seed=4, B=3, lo=100, hi=2500)),
+}
+
+
+@pytest.mark.parametrize("case", list(STREAM_K_CASES))
+def test_stream_k_schedule_matches_oracle(gpu, case):
+    wl = STREAM_K_CASES[case]()
+    _run_and_check(wl, gpu, kv_split=-2, label=f"stream-k-{case}")
+    if case.startswith("reference"):
+        _run_and_check(wl, gpu, kv_split=-2, one_word=True, label=f"stream-k-{case}-int64-mask")
+
+
+def _call(wl, dev, kv_split, qkv=None):
+    from cast_amd import varlen_tree_attention
+    q, k, v = qkv if qkv is not None else wl.qkv(device=dev)
+    meta = wl.meta_tensors(dev)
+    mask = torch.from_numpy(_words(wl).view(np.int64).copy()).to(dev)
+    out, lse = varlen_tree_attention(q, k, v, meta["cu_q"], meta["cu_kv"], meta["prefix_len"], meta["pack_len"],
+                                     mask, return_lse=True, kv_split=kv_split, check=True)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def test_schedule_choice_ragged_and_uniform(gpu):
+    # The library's own choice (kv_split=0) keeps the static splits on the
+    # benchmark's ragged batch (bit for bit the forced chunk); the forced
+    # stream-K schedule cuts other pieces (other bits, within the bar).  The
+    # uniform headline batch keeps its static splits too.
+    from cast_amd.tree_attn import plan
+    wl = SC.qwen3_ragged(seed=0)
+    print(f"case schedule-choice ragged: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv}", flush=True)
+    qkv = wl.qkv(device=gpu)
+    chunk = plan(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D).kv_split
+    auto, sk, static = (_call(wl, gpu, s, qkv) for s in (0, -2, chunk))
+    assert torch.equal(auto[0], static[0]) and torch.equal(auto[1], static[1])
+    assert not torch.equal(sk[0], static[0])
+    assert (sk[0].float() - static[0].float()).abs().max() <= 2e-2
+    wl = SC.qwen3_headline()
+    print("case schedule-choice headline", flush=True)
+    qkv = wl.qkv(device=gpu, generator_device=gpu)
+    chunk = plan(wl.B, wl.total_q, wl.total_kv, wl.Hq, wl.Hkv, wl.D).kv_split
+    auto, static = (_call(wl, gpu, s, qkv) for s in (0, chunk))
+    assert torch.equal(auto[0], static[0]) and torch.equal(auto[1], static[1])
+
+
+def test_stream_k_exact_scaling_property(gpu):
+    # V -> 2V (exact in bf16) doubles the output and keeps the LSE, bit for
+    # bit, through the stream-K partials and their merge
+    wl = SC.qwen3_ragged(seed=0)
+    print("case stream-k-scaling", flush=True)
+    q, k, v = wl.qkv(device=gpu)
+    out, lse = _call(wl, gpu, -2, (q, k, v))
+    out2, lse2 = _call(wl, gpu, -2, (q, k, v * 2))
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    assert torch.equal(out2, out * 2) and torch.equal(lse2, lse)

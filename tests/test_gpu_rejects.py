@@ -59,7 +59,7 @@ def _check(wl, q, k, v, words, out, lse, accepted):
             assert torch.all(torch.isneginf(l[rows])), f"rejected request {b} lse not -inf"
 
 
-@pytest.mark.parametrize("kv_split", [0, -1, 128])
+@pytest.mark.parametrize("kv_split", [0, -1, 128, -2])
 def test_pack_longer_than_one_mask_word(gpu, kv_split):
     from cast_amd import varlen_tree_attention
     wl, q, k, v, words = _setup(gpu, [10, 100, 20], [300, 50, 700])
@@ -122,7 +122,7 @@ def test_overlapping_packs_reject_the_batch(gpu):
     _check(wl, q, k, v, words, out, lse, accepted=[])
 
 
-@pytest.mark.parametrize("kv_split", [0, -1])
+@pytest.mark.parametrize("kv_split", [0, -1, -2])
 def test_store_batch_above_total_kv(gpu, kv_split):
     from cast_amd.tree_attn import store_tree_attention
     wl, q, k, v, words = _setup(gpu, [10, 40, 20], [300, 50, 700], seed=3)

@@ -110,7 +110,7 @@ def test_random_configurations(gpu, seed):
     dt = str(rng.choice(["bf16", "fp16", "fp32"]))
     B = int(rng.choice([1, 3, 8, 40, 70]))
     s_hi = int(rng.choice([2, 300, 2500]))
-    split = int(rng.choice([0, 64, 320, -1]))
+    split = int(rng.choice([0, 64, 320, -1, -2]))
     wl = SC.random_parent_batch(seed=seed, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, s_lo=0, s_hi=s_hi, p_lo=1, p_hi=129,
                                 dtype=dt, qkv_scale=0.5)
     requests = sorted(rng.choice(B, size=min(B, 3), replace=False).tolist())
@@ -127,7 +127,7 @@ def test_store_empty_and_tiny_prefixes(gpu):
 
 def test_store_ragged_split_k(gpu):
     wl = SC.qwen3_ragged(seed=4, B=4, lo=300, hi=5000)
-    for split in (0, 64, 1000, -1):
+    for split in (0, 64, 1000, -1, -2):
         _check_store(wl, gpu, kv_split=split, requests=[0, 3], label=f"store-ragged-split{split}")
 
 
