@@ -80,6 +80,28 @@ def roofline(wl, seconds):
                 frac=round(ach / (PEAK_HBM / 1e9), 4))
 
 
+def traffic_of(name):
+    """HBM bytes of one call over workload ``name`` as the profiler's FETCH_SIZE
+    and WRITE_SIZE counters read them, per kernel, scaled by the same
+    counters over a plain elementwise kernel (profiles/traffic.json), or
+    None when that workload was not profiled."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text()).get(name)
+    except (ValueError, OSError):
+        return None
+
+
+def whole_call_traffic(wl, entry):
+    """Attention kernel plus split-K combine: bytes and their ratio to the
+    workload's algorithmic bytes (Q, K, V, out and the ancestor words once)."""
+    if not entry:
+        return None
+    total = entry["hbm_bytes_per_launch"] + entry.get("combine_bytes", 0)
+    return dict(bytes=total, ratio=round(total / wl.algorithmic_bytes(), 3),
+                attention_bytes=entry["hbm_bytes_per_launch"], combine_bytes=entry.get("combine_bytes", 0),
+                algorithmic_bytes=wl.algorithmic_bytes())
+
+
 class Harness:
     """Resident inputs of one workload, with rotated K/V sets."""
 
@@ -180,6 +202,40 @@ def cpu_baseline(wl, budget_s=12.0):
                 sample=f"request 0 of {wl.B} (S={S0}, P={P0}, {wl.Hq}/{wl.Hkv} heads, D={wl.D}): dense fp32 "
                        f"torch oracle on the bf16-rounded inputs, median of {len(times)} runs "
                        f"({med * 1e3:.1f} ms each), scaled x{wl.B}")
+
+
+def cpu_baseline_sample(wl, budget_s=2.0):
+    """The oracle on host cores over a bounded sample of ``wl``'s requests:
+    requests 0, 1, ... are each run once per pass until ``budget_s`` is
+    spent, and the median per request is scaled to the whole batch by the
+    requests' score counts P_b * (S_b + P_b)."""
+    import torch
+    from oracle import attn as oracle_attn
+    from oracle import bitmask as oracle_bitmask
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, k, v = wl.qkv(device="cpu")
+    words = oracle_bitmask.chain_walk_words(wl.packed.parent, wl.cu_q)
+    qf, kf, vf = q.float(), k.float(), v.float()
+    work = [int(wl.pack_len[b]) * (int(wl.prefix_len[b]) + int(wl.pack_len[b])) for b in range(wl.B)]
+    times = {}
+    t_end = time.perf_counter() + budget_s
+    b = 0
+    while True:
+        t = time.perf_counter()
+        oracle_attn.dense_tree_attention(qf, kf, vf, wl.cu_q, wl.cu_kv, wl.prefix_len, wl.pack_len, words,
+                                         requests=[b])
+        times.setdefault(b, []).append(time.perf_counter() - t)
+        b = (b + 1) % wl.B
+        if time.perf_counter() > t_end or len(times[b] if b in times else []) >= 50:
+            break
+    sampled = sorted(times)
+    med = sum(statistics.median(times[r]) for r in sampled)
+    scale = sum(work) / sum(work[r] for r in sampled)
+    runs = sum(len(x) for x in times.values())
+    return dict(value=round(med * scale * 1e6, 1), unit="us/call", cores=cores, kind="port",
+                sample=f"requests {sampled[0]}-{sampled[-1]} of {wl.B} ({runs} runs, median per request), dense "
+                       f"fp32 torch oracle, scaled x{scale:.3g} by score count")
 
 
 def store_layout(dev, steps, warmup):
@@ -521,11 +577,14 @@ def bitmask_lines(dev, steps, warmup):
 
 
 ATTN_WORKLOADS = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
-                  "qwen3-8b-stress-b32", "qwen3-8b-b8-ctx8k-p128-fp32", "qwen3-8b-b8-ctx8k-p128-fp16",
-                  "d256-b8-ctx8k-p128")
+                  "qwen3-8b-stress-b32", "qwen3-8b-stress-b32-trees", "qwen3-8b-b8-ctx8k-p128-fp32",
+                  "qwen3-8b-b8-ctx8k-p128-fp16", "d256-b8-ctx8k-p128")
+# the benchmark's five named configurations, each with a CPU oracle figure
+CPU_SAMPLED = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
+               "qwen3-8b-stress-b32")
 
 
-def attn_workload(dev, name, steps, warmup):
+def attn_workload(dev, name, steps, warmup, cpu=False):
     """One attention workload timed like the headline (2 rotated K/V sets)."""
     import torch
     from cast_amd import scenarios
@@ -540,32 +599,37 @@ def attn_workload(dev, name, steps, warmup):
     t = h.time(steps, warmup)
     rl = roofline(wl, t["attn_us"] * 1e-6)
     res = dict(us_per_call=round(t["call_us"], 2), attn_us=round(t["attn_us"], 2),
-               combine_us=round(t["combine_us"], 2), dtype=wl.dtype, bound=rl["bound"], frac=rl["frac"],
+               combine_us=round(t["combine_us"], 2), steps=steps, warmup=warmup, dtype=wl.dtype,
+               bound=rl["bound"], frac=rl["frac"],
                hbm_frac=round(wl.algorithmic_bytes() / (t["call_us"] * 1e-6) / PEAK_HBM, 4),
                tokens=int(wl.total_q), kv_tokens=int(wl.total_kv), kv_split=h.plan.kv_split,
-               algorithmic_bytes=wl.algorithmic_bytes(), algorithmic_flops=wl.algorithmic_flops())
+               algorithmic_bytes=wl.algorithmic_bytes(), algorithmic_flops=wl.algorithmic_flops(),
+               whole_call_traffic=whole_call_traffic(wl, traffic_of(name)))
     log(f"  {name}: {t['call_us']:.1f} us/call (attn {t['attn_us']:.1f}, combine {t['combine_us']:.1f}), "
-        f"{rl['bound']} frac {rl['frac']:.3f}")
+        f"{rl['bound']} frac {rl['frac']:.3f} ({steps} timed after {warmup})")
     del h
     torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline_sample(wl)
+        log(f"    cpu oracle: {res['cpu_baseline']['value']:.0f} us/call ({res['cpu_baseline']['sample']})")
     return res
 
 
-def secondary(dev, steps, warmup):
-    import torch
-    from cast_amd import greedy_accept, scenarios, tree_bitmask
+def secondary(dev, steps, warmup, cpu=True):
+    """Every other workload, each entry with the timed and untimed call
+    counts it used."""
     res = {}
     for name in ATTN_WORKLOADS:
-        res[name] = attn_workload(dev, name, steps, warmup)
-    # the store path is the headline's attention on another layout: timed with
-    # the headline's step and warmup counts (fresh stores settle over ~20 calls)
-    res["store_layout"] = store_layout(dev, max(steps, 60), max(warmup, 20))
-    res["kv_append"] = kv_append(dev, steps, warmup)
-    res["cache_gather"] = cache_gather(dev, steps, warmup)
-    res["draft_trees"] = draft_trees(dev, steps, warmup)
-    res["graph_replay"] = graph_replay(dev, steps, warmup)
-    res["verify_round"] = verify_round(dev, steps, warmup)
-    res.update(bitmask_lines(dev, steps, warmup))
+        res[name] = attn_workload(dev, name, steps, warmup, cpu=cpu and name in CPU_SAMPLED)
+    # fresh stores settle over ~20 calls
+    runs = [("store_layout", store_layout, max(steps, 60), max(warmup, 20)),
+            ("kv_append", kv_append, steps, warmup), ("cache_gather", cache_gather, steps, warmup),
+            ("draft_trees", draft_trees, steps, warmup), ("graph_replay", graph_replay, steps, warmup),
+            ("verify_round", verify_round, steps, warmup)]
+    for key, fn, n, w in runs:
+        res[key] = dict(fn(dev, n, w), steps=n, warmup=w)
+    for key, r in bitmask_lines(dev, steps, warmup).items():
+        res[key] = dict(r, steps=steps, warmup=warmup)
     return res
 
 
@@ -758,13 +822,8 @@ def main():
     # achieved = algorithmic work per launch / mean launch duration (HIP events
     # on the launch stream), comparable with the profiler's average duration
     rl = roofline(wl, t["attn_mean_us"] * 1e-6)
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        try:
-            traffic = json.loads(TRAFFIC_FILE.read_text()).get(wl.name, {}).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
-    rl["traffic"] = traffic
+    entry = traffic_of(wl.name)
+    rl["traffic"] = entry["hbm_bytes_per_launch"] if entry else None
     call_s = t["call_us"] * 1e-6
     line = {
         "metric": METRIC, "value": round(t["call_us"], 2), "unit": "us/call", "n_gpus": 1,
@@ -785,6 +844,8 @@ def main():
         "attn_kernel_us": round(t["attn_us"], 2), "combine_us": round(t["combine_us"], 2),
         "call_mean_us": round(t["call_mean_us"], 2), "host_wall_us": round(t["wall_us"], 2),
         "algorithmic_bytes": wl.algorithmic_bytes(), "algorithmic_flops": wl.algorithmic_flops(),
+        # the attention kernel's bytes (roofline.traffic) plus the combine's
+        "whole_call_traffic": whole_call_traffic(wl, entry),
     }
     # the practical MFMA ceiling of this launch shape, timed right after the
     # headline calls with the same step and warmup counts: the headline's MFMA
@@ -800,7 +861,9 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_secondary:
         log("secondary workloads:")
-        line["secondary"] = secondary(dev, max(10, args.steps // 3), max(3, args.warmup // 3))
+        # at least 50 timed calls each, whatever the headline's counts
+        line["secondary"] = secondary(dev, max(50, args.steps // 2), max(20, args.warmup // 4),
+                                      cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)...")
         line["cpu_baseline"] = cpu_baseline(wl)

@@ -421,6 +421,20 @@ __device__ __forceinline__ uint32_t vis_window(uint64_t w0, uint64_t w1, int j0)
     return (uint32_t)v;
 }
 
+// The highest pack key that ancestor words (w0, w1) make visible, or -1.
+__device__ __forceinline__ int last_visible(uint64_t w0, uint64_t w1) {
+    return w1 ? 127 - __builtin_clzll(w1) : (w0 ? 63 - __builtin_clzll(w0) : -1);
+}
+
+// Whether any row of the wave sees a key of the 32-key block that starts at
+// pack key j0, of which the first `lim` keys are real.  A block that no row
+// sees adds exact zeros to every row's sum and output, so it can be skipped.
+__device__ __forceinline__ bool block_live(uint64_t w0, uint64_t w1, int j0, int lim) {
+    uint32_t vis = vis_window(w0, w1, j0);
+    vis &= lim >= 32 ? ~0u : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+    return __any(vis != 0u);
+}
+
 // What the MFMA kernel's epilogue needs, parked in LDS during the key loop
 // so that it holds no scalar registers there.
 struct EpiArgs {
@@ -703,6 +717,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[NBUF][BN * KPAD];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[NBUF][D * VPAD];
     __shared__ EpiArgs epi;
+    __shared__ int pack_hi[WAVES];   // per wave: the last pack key a row of it sees
     // Head dim 256 (one wave per SIMD, no registers to spare) has no
     // stream-K instance.
     constexpr bool kStreamK = SKI && D <= 128;
@@ -824,7 +839,6 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     const int n_pre = k_begin < pre_end ? (pre_end - k_begin + BN - 1) / BN : 0;
     const int pk_begin = max(k_begin, sq.S);
     const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
-    const int ntiles = n_pre + n_pack;
     auto tile_t0 = [&](int t) __attribute__((always_inline)) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
     auto tile_valid = [&](int t) __attribute__((always_inline)) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
     auto fetch = [&](int t) __attribute__((always_inline)) { fetch_tile(kv, sq, tile_t0(t)); };
@@ -858,6 +872,14 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 
     // the previous segment's epilogue (its reads of epi) and LDS tiles retire
     if (!first_seg) __syncthreads();
+    // Pack tiles past the last pack key any row of the workgroup sees are
+    // skipped: a one-unit workgroup at head dims up to 128 (the stream-K
+    // segments keep their tiles; head dim 256 has no registers to spare)
+    constexpr bool kTrimPack = !kStreamK && D <= 128;
+    if (kTrimPack && n_pack > 0) {
+        const int hi = wave_max(last_visible(mw0, mw1));
+        if (lane == 0) pack_hi[wave] = hi;
+    }
     if (tid == 0) {
         epi.out = a.out;
         epi.lse = a.lse;
@@ -874,6 +896,16 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         epi.Hq = a.Hq;
     }
     __syncthreads();
+    int n_pack_live = n_pack;
+    if (kTrimPack && n_pack > 0) {
+        int hi = pack_hi[0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) hi = max(hi, pack_hi[w]);
+        const int pk0 = pk_begin - sq.S;
+        n_pack_live = hi < pk0 ? 0 : min(n_pack, (hi - pk0) / BN + 1);
+    }
+    // (read from LDS, so held in a vector register: made scalar again)
+    const int ntiles = __builtin_amdgcn_readfirstlane(n_pre + n_pack_live);
     // ---- the three stages of a tile
     // S^T = K Q^T: two 32-key blocks x 32 queries
     auto qk = [&](int buf, floatx16 (&s)[2]) __attribute__((always_inline)) {
@@ -982,6 +1014,14 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, kQkAhead, 1);
     };
 
+    auto tile_body = [&](int t, int buf) __attribute__((always_inline)) {
+        floatx16 s[2];
+        vec8 pb[2][2];
+        qk(buf, s);
+        softmax(t, s, pb);
+        pv(buf, pb);
+    };
+
     // The next tile's loads are in flight during the current tile's MFMA
     // work.  During a stream-K segment's last tile, the next segment's first
     // tile and (once this tile's QK product is issued) its Q are loaded.
@@ -996,11 +1036,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         __syncthreads();
         fetch(t + 1);
         if (!active) continue;
-        floatx16 s[2];
-        vec8 pb[2][2];
-        qk(buf, s);
-        softmax(t, s, pb);
-        pv(buf, pb);
+        tile_body(t, buf);
     }
     if (ntiles > 0) {
         const int t = ntiles - 1;
@@ -1014,13 +1050,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
                 fetch_tile(kvn, nxt.sq, nxt.k_begin);
             }
         }
-        if (active) {
-            floatx16 s[2];
-            vec8 pb[2][2];
-            qk(buf, s);
-            softmax(t, s, pb);
-            pv(buf, pb);
-        }
+        if (active) tile_body(t, buf);
         // the next segment's Q: its latency overlaps this segment's epilogue
         if (kPrefetchNext && has_next) {
             __builtin_amdgcn_sched_barrier(0);
@@ -1034,11 +1064,7 @@ void tree_attn_mfma_kernel(AttnArgs a) {
         __syncthreads();
         if (t + 1 < ntiles) fetch(t + 1);
         if (!active) continue;
-        floatx16 s[2];
-        vec8 pb[2][2];
-        qk(buf, s);
-        softmax(t, s, pb);
-        pv(buf, pb);
+        tile_body(t, buf);
     }
     }
 
@@ -1127,6 +1153,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float Ks[2][BN * KPAD];
     __shared__ __attribute__((aligned(16))) float Vs[2][BN * KPAD];
     __shared__ EpiArgs epi;
+    __shared__ int pack_hi[WAVES];   // per wave: the last pack key a row of it sees
     __shared__ SkReq skr[SKI ? 64 : 1];
 
     Unit wu;
@@ -1177,7 +1204,6 @@ void tree_attn_f32_kernel(AttnArgs a) {
     const int n_pre = k_begin < pre_end ? (pre_end - k_begin + BN - 1) / BN : 0;
     const int pk_begin = max(k_begin, sq.S);
     const int n_pack = k_end > pk_begin ? (k_end - pk_begin + BN - 1) / BN : 0;
-    const int ntiles = n_pre + n_pack;
     auto tile_t0 = [&](int t) __attribute__((always_inline)) { return t < n_pre ? k_begin + t * BN : pk_begin + (t - n_pre) * BN; };
     auto tile_valid = [&](int t) __attribute__((always_inline)) { return min(BN, (t < n_pre ? pre_end : k_end) - tile_t0(t)); };
 
@@ -1244,6 +1270,12 @@ void tree_attn_f32_kernel(AttnArgs a) {
         }
     };
 
+    // pack tiles past the last pack key any row of the workgroup sees are
+    // skipped (a one-unit workgroup; the stream-K segments keep their tiles)
+    if (!SKI && n_pack > 0) {
+        const int hi = wave_max(last_visible(mw0, mw1));
+        if (lane == 0) pack_hi[wave] = hi;
+    }
     if (tid == 0) {
         epi.out = a.out;
         epi.lse = a.lse;
@@ -1260,6 +1292,16 @@ void tree_attn_f32_kernel(AttnArgs a) {
         epi.Hq = a.Hq;
     }
     __syncthreads();
+    int n_pack_live = n_pack;
+    if (!SKI && n_pack > 0) {
+        int hi = pack_hi[0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) hi = max(hi, pack_hi[w]);
+        const int pk0 = pk_begin - sq.S;
+        n_pack_live = hi < pk0 ? 0 : min(n_pack, (hi - pk0) / BN + 1);
+    }
+    // (read from LDS, so held in a vector register: made scalar again)
+    const int ntiles = __builtin_amdgcn_readfirstlane(n_pre + n_pack_live);
 
     if (ntiles > 0) fetch(0);
     for (int t = 0; t < ntiles; ++t) {
@@ -1268,22 +1310,47 @@ void tree_attn_f32_kernel(AttnArgs a) {
         __syncthreads();
         if (t + 1 < ntiles) fetch(t + 1);
         if (!active) continue;
-        // S^T = K Q^T, the two 32-key blocks' chains interleaved
-        floatx16 s[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-        for (int i = 0; i < DH / 4; ++i) {
-            const floatx4 k0 = *reinterpret_cast<const floatx4 *>(&Ks[buf][l32 * KPAD + DH * g + 4 * i]);
-            const floatx4 k1 = *reinterpret_cast<const floatx4 *>(&Ks[buf][(32 + l32) * KPAD + DH * g + 4 * i]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0[j], qf[4 * i + j], s[0], 0, 0, 0);
-                s[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1[j], qf[4 * i + j], s[1], 0, 0, 0);
-            }
-        }
-        // visibility on pack tiles and partial tiles (as in the bf16 kernel)
         const int t0 = tile_t0(t);
         const int valid = tile_valid(t);
         const bool pack_tile = t >= n_pre;
+        // in a pack tile, the 32-key blocks no row of the wave sees are
+        // skipped: scores -inf, no PV product
+        bool live[2] = {true, true};
+        if (!SKI && pack_tile) {
+            live[0] = block_live(mw0, mw1, t0 - sq.S, valid);
+            live[1] = block_live(mw0, mw1, t0 - sq.S + 32, valid - 32);
+        }
+        // S^T = K Q^T, the two 32-key blocks' chains interleaved
+        floatx16 s[2] = {floatx16{}, floatx16{}};
+        if (live[0] && live[1]) {
+#pragma unroll
+            for (int i = 0; i < DH / 4; ++i) {
+                const floatx4 k0 = *reinterpret_cast<const floatx4 *>(&Ks[buf][l32 * KPAD + DH * g + 4 * i]);
+                const floatx4 k1 = *reinterpret_cast<const floatx4 *>(&Ks[buf][(32 + l32) * KPAD + DH * g + 4 * i]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0[j], qf[4 * i + j], s[0], 0, 0, 0);
+                    s[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1[j], qf[4 * i + j], s[1], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                if (!live[kb]) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) s[kb][e] = -INFINITY;
+                    continue;
+                }
+#pragma unroll
+                for (int i = 0; i < DH / 4; ++i) {
+                    const floatx4 kk = *reinterpret_cast<const floatx4 *>(&Ks[buf][(kb * 32 + l32) * KPAD + DH * g + 4 * i]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[j], qf[4 * i + j], s[kb], 0, 0, 0);
+                }
+            }
+        }
+        // visibility on pack tiles and partial tiles (as in the bf16 kernel)
         if (pack_tile || valid < BN) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
@@ -1324,7 +1391,8 @@ void tree_attn_f32_kernel(AttnArgs a) {
         lsum += acc;
         // O^T += V^T P^T: step e of block kb is key 32*kb + 8*(e/4) + 4*g + e%4
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb) {
+            if (!live[kb]) continue;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int key = kb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
@@ -1333,6 +1401,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
                 for (int db = 0; db < DB; ++db)
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[db], s[kb][e], o[db], 0, 0, 0);
             }
+        }
     }
 
     if (active && qvalid) {

@@ -199,6 +199,13 @@ def stress_mixed(seed=0, B=32, lo=256, hi=4096, pack=128):
     return _make("qwen3-8b-stress-b32", trees, prefix, QWEN3_8B, "bf16", seed, 1 / math.sqrt(128))
 
 
+def stress_trees_only(seed=0):
+    """The stress batch's 32 trees (4096 packed tree tokens) with no prefix:
+    every key tile is a tree-tree tile, so the masked block runs alone."""
+    wl = stress_mixed(seed)
+    return _make("qwen3-8b-stress-b32-trees", wl.trees, [0] * wl.B, QWEN3_8B, "bf16", seed, 1 / math.sqrt(128))
+
+
 def random_parent_batch(seed=0, B=8, Hq=32, Hkv=8, D=128, s_lo=200, s_hi=400, p_lo=2, p_hi=64,
                         dtype="fp32", qkv_scale=1.0):
     """Random-parent packs, ``parent[i] ~ U[0, i)``, like the kernel test of
@@ -261,6 +268,7 @@ CONFIGS = {
     "qwen3-8b-b8-ctx8k-p128": qwen3_headline,
     "llama31-8b-ctx32k-p128": llama_long,
     "qwen3-8b-stress-b32": stress_mixed,
+    "qwen3-8b-stress-b32-trees": stress_trees_only,
     "d256-b8-ctx8k-p128": head_dim_256,
 }
 

@@ -26,12 +26,12 @@ def _words(wl):
 
 
 def _run_and_check(wl, dev, requests=None, kv_heads=None, kv_split=0, one_word=False, q_noncontig=False,
-                   label="", qkv=None, reference_bar=False):
+                   label="", qkv=None, reference_bar=False, words=None):
     from cast_amd import varlen_tree_attention
     print(f"case {label or wl.name}: B={wl.B} total_q={wl.total_q} total_kv={wl.total_kv} "
           f"Hq={wl.Hq} Hkv={wl.Hkv} D={wl.D} {wl.dtype} split={kv_split}", flush=True)
     q, k, v = wl.qkv(device=dev) if qkv is None else (x.to(dev) for x in qkv)
-    words = _words(wl)
+    words = _words(wl) if words is None else words
     if one_word:
         assert not words[:, 1].any()
         mask_dev = torch.from_numpy(words[:, 0].view(np.int64).copy()).to(dev)
@@ -403,3 +403,75 @@ def test_stream_k_exact_scaling_property(gpu):
     out2, lse2 = _call(wl, gpu, -2, (q, k, v * 2))
     assert torch.isfinite(out).all() and torch.isfinite(lse).all()
     assert torch.equal(out2, out * 2) and torch.equal(lse2, lse)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("kind", ["far-below", "far-above", "mixed"])
+def test_extreme_score_ranges(gpu, dtype, kind):
+    # The kernel's online softmax only rescales once a tile's max exceeds
+    # the running max by a slack of 2^8, and packs probabilities into the
+    # 16-bit format before the PV product.  Scores far below zero, far above
+    # it and rows of both kinds in one wave, against the oracle: the
+    # probabilities must neither overflow the format nor flush to zero.
+    # Keys share a direction u with weight 6; queries lie along +u or -u
+    # with weight w, so scaled scores sit near +-6 w / sqrt(D).
+    wl = SC.random_parent_batch(seed=21, B=3, Hq=8, Hkv=2, D=128, s_lo=300, s_hi=1500, p_lo=20, p_hi=129,
+                                dtype=dtype, qkv_scale=0.3)
+    q, k, v = wl.qkv(device="cpu")
+    g = torch.Generator().manual_seed(5)
+    u = torch.randn(wl.D, generator=g)
+    u /= u.norm()
+    w = {"bf16": 100.0, "fp16": 24.0}[dtype]   # scaled scores about 76 and 18 in log2 units
+    k = (k.float() + 6.0 * u).to(k.dtype)
+    sign = {"far-below": -1.0, "far-above": 1.0}.get(kind)
+    if sign is None:
+        sign = torch.where(torch.arange(wl.total_q) % 3 == 0, 1.0, -1.0)[:, None, None]
+    q = (q.float() + sign * w * u).to(q.dtype)
+    print(f"case extreme-scores {kind} {dtype}: scaled score ~ {float(6 * w / math.sqrt(wl.D)):.1f}", flush=True)
+    _run_and_check(wl, gpu, qkv=(q, k, v), label=f"extreme-scores-{kind}-{dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_tree_block_alone(gpu, dtype):
+    # the stress batch's 32 trees with no prefix: every tile is a pack tile,
+    # and the pack tiles past the last key a workgroup's rows see are skipped
+    import dataclasses
+    wl = SC.stress_trees_only()
+    if dtype == "fp32":
+        wl = dataclasses.replace(wl, dtype="fp32", qkv_scale=1.0)
+    _run_and_check(wl, gpu, label=f"tree-block-alone-{dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("kv_split", [0, 64])
+def test_arbitrary_visibility_words(gpu, dtype, kv_split):
+    # Visibility words that no tree produces: random bits anywhere in the
+    # pack (above a row's own index too), rows that see no pack key, rows
+    # that see only the last pack key, and one-sided 64-key halves.  Skipped
+    # pack tiles and blocks are decided from the words themselves, so every
+    # case matches the oracle on the same words.
+    wl = SC.random_parent_batch(seed=17, B=6, Hq=8, Hkv=2, D=128, s_lo=0, s_hi=300, p_lo=1, p_hi=129,
+                                dtype=dtype)
+    rng = np.random.default_rng(4)
+    words = np.zeros((wl.total_q, 2), dtype=np.uint64)
+    for b in range(wl.B):
+        P, q0 = int(wl.pack_len[b]), int(wl.cu_q[b])
+        for i in range(P):
+            kind = (b + i) % 5
+            if kind == 0:
+                bits = rng.random(P) < 0.3                       # random, any position
+            elif kind == 1:
+                bits = np.zeros(P, dtype=bool)                   # no pack key
+            elif kind == 2:
+                bits = np.zeros(P, dtype=bool)
+                bits[P - 1] = True                               # only the last pack key
+            elif kind == 3:
+                bits = np.zeros(P, dtype=bool)
+                bits[: min(P, 64)] = rng.random(min(P, 64)) < 0.5    # first half only
+            else:
+                bits = np.zeros(P, dtype=bool)
+                bits[64:] = rng.random(max(0, P - 64)) < 0.5         # second half only
+            for j in np.flatnonzero(bits):
+                words[q0 + i, j >> 6] |= np.uint64(1) << np.uint64(j & 63)
+    print(f"case arbitrary-words {dtype} split={kv_split}: B={wl.B} total_q={wl.total_q}", flush=True)
+    _run_and_check(wl, gpu, kv_split=kv_split, words=words, label=f"arbitrary-words-{dtype}-{kv_split}")
