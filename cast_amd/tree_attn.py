@@ -5,7 +5,8 @@ positional signature, argument meaning and result, with these additions
 (keyword-only, all optional):
 
   return_lse  also return the natural-log log-sum-exp [total_q, Hq] (fp32)
-  kv_split    keys per split-K chunk (0: library heuristic, <0: no split)
+  kv_split    keys per split-K chunk (0: library heuristic, SPLIT_STREAM:
+              the stream-K schedule, other values < 0: no split)
   check       synchronise once and raise ValueError if the kernels flagged
               inconsistent metadata (off by default: the call never syncs)
   out         preallocated output [total_q, Hq, D]
@@ -35,6 +36,8 @@ import torch
 from . import _lib
 
 _DTYPES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.FP16, torch.float32: _lib.FP32}
+# kv_split value asking for the stream-K schedule (CAST_SPLIT_STREAM in the C header)
+SPLIT_STREAM = -2
 
 
 def _as_i32(x, device):

@@ -100,16 +100,14 @@ int cast_tree_bitmask(const int32_t *parent, const int32_t *cu_q, int32_t batch,
  *   kv_split  keys per split-K chunk (multiple of 64); 0 lets the library
  *             choose; CAST_SPLIT_STREAM (-2) asks for the stream-K schedule;
  *             any other negative value disables split-K.  With 0 the library
- *             cuts long prefixes into equal splits, and for batches of up to
- *             64 requests whose splits would leave the GPU unbalanced
- *             (ragged prefixes), the kernels take the stream-K schedule
- *             instead: pairs of workgroups on one XCD get equal ranges of
- *             key tiles over all (request, KV head, row block) units, and a
- *             combine merges the pieces of units cut between workgroups.
- *             That choice is made on the device from the metadata.  The
- *             static schedule sums each request's keys in an order that only
- *             depends on batch totals; stream-K's cut points follow the batch
- *             order.
+ *             cuts long prefixes into equal splits so that the work items
+ *             cover the device's CUs (static schedule, longest items first).
+ *             Stream-K (only when asked for): pairs of workgroups on one XCD
+ *             get equal ranges of key tiles over all (request, KV head, row
+ *             block) units, and a combine merges the pieces of units cut
+ *             between workgroups; the pieces' cut points follow the batch
+ *             order.  The static schedule sums each request's keys in an
+ *             order that only depends on batch totals.
  *   workspace / workspace_bytes  scratch of at least
  *             cast_tree_attn_workspace_size(...) bytes, 256-byte aligned
  *   status    int32*, nullable device status word

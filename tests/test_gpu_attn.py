@@ -318,8 +318,8 @@ def test_fp32_large_configs_sampled(gpu):
         _run_and_check(wl, gpu, requests=reqs, kv_heads=[0, 5], label=wl.name)
 
 
-# ---- the stream-K schedule (kv_split=-2 asks for it; the library also takes
-# it by itself when the static splits are unbalanced)
+# ---- the stream-K schedule (kv_split=-2 asks for it; the library's own
+# choice, kv_split=0, is always the static schedule)
 
 def _edges(dtype="bf16"):
     from cast_amd.tree import TreeNode
