@@ -613,8 +613,8 @@ __device__ bool sk_next_segment(const AttnArgs &a, WorkCursor &cur, Unit &u, con
 
 // The first piece of work of the calling workgroup, after the batch
 // prologue; false when it has none (or the batch was rejected).  Batches of
-// up to 64 requests take the stream-K lanes when sk_plan chooses them, else
-// the longest-first schedule; larger ones take items in batch order,
+// up to 64 requests take the stream-K lanes when the caller asked for them
+// and sk_plan accepts the batch, else the longest-first schedule; larger ones take items in batch order,
 // consecutive items (the row blocks of one key split) on one XCD so that
 // they share its L2.  skr: LDS for the stream-K table (64 entries).
 template <bool SK>   // SK: the kernel instance takes the stream-K schedule when the plan asks
