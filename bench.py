@@ -204,11 +204,12 @@ def cpu_baseline(wl, budget_s=12.0):
                        f"({med * 1e3:.1f} ms each), scaled x{wl.B}")
 
 
-def cpu_baseline_sample(wl, budget_s=2.0):
+def cpu_baseline_sample(wl, budget_s=2.0, min_runs=10, warmup=3):
     """The oracle on host cores over a bounded sample of ``wl``'s requests:
-    requests 0, 1, ... are each run once per pass until ``budget_s`` is
-    spent, and the median per request is scaled to the whole batch by the
-    requests' score counts P_b * (S_b + P_b)."""
+    after ``warmup`` untimed runs of request 0, requests 0, 1, ... are each
+    run once per pass until ``budget_s`` is spent and at least ``min_runs``
+    runs are timed; the median per request is scaled to the whole batch by
+    the requests' score counts P_b * (S_b + P_b)."""
     import torch
     from oracle import attn as oracle_attn
     from oracle import bitmask as oracle_bitmask
@@ -218,24 +219,30 @@ def cpu_baseline_sample(wl, budget_s=2.0):
     words = oracle_bitmask.chain_walk_words(wl.packed.parent, wl.cu_q)
     qf, kf, vf = q.float(), k.float(), v.float()
     work = [int(wl.pack_len[b]) * (int(wl.prefix_len[b]) + int(wl.pack_len[b])) for b in range(wl.B)]
-    times = {}
-    t_end = time.perf_counter() + budget_s
-    b = 0
-    while True:
-        t = time.perf_counter()
+
+    def run(b):
         oracle_attn.dense_tree_attention(qf, kf, vf, wl.cu_q, wl.cu_kv, wl.prefix_len, wl.pack_len, words,
                                          requests=[b])
+
+    for _ in range(warmup):
+        run(0)
+    times = {}
+    t_end = time.perf_counter() + budget_s
+    b, runs = 0, 0
+    while True:
+        t = time.perf_counter()
+        run(b)
         times.setdefault(b, []).append(time.perf_counter() - t)
+        runs += 1
         b = (b + 1) % wl.B
-        if time.perf_counter() > t_end or len(times[b] if b in times else []) >= 50:
+        if (time.perf_counter() > t_end and runs >= min_runs) or len(times.get(b, [])) >= 50:
             break
     sampled = sorted(times)
     med = sum(statistics.median(times[r]) for r in sampled)
     scale = sum(work) / sum(work[r] for r in sampled)
-    runs = sum(len(x) for x in times.values())
     return dict(value=round(med * scale * 1e6, 1), unit="us/call", cores=cores, kind="port",
-                sample=f"requests {sampled[0]}-{sampled[-1]} of {wl.B} ({runs} runs, median per request), dense "
-                       f"fp32 torch oracle, scaled x{scale:.3g} by score count")
+                sample=f"requests {sampled[0]}-{sampled[-1]} of {wl.B} ({runs} timed runs after {warmup} "
+                       f"warmups, median per request), dense fp32 torch oracle, scaled x{scale:.3g} by score count")
 
 
 def store_layout(dev, steps, warmup):
