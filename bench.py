@@ -585,7 +585,7 @@ def bitmask_lines(dev, steps, warmup):
 
 ATTN_WORKLOADS = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
                   "qwen3-8b-stress-b32", "qwen3-8b-stress-b32-trees", "qwen3-8b-b8-ctx8k-p128-fp32",
-                  "qwen3-8b-b8-ctx8k-p128-fp16", "d256-b8-ctx8k-p128")
+                  "qwen3-8b-b8-ctx8k-p128-fp16", "d256-b8-ctx8k-p128", "d256-b8-ctx8k-p128-fp32")
 # the benchmark's five named configurations, each with a CPU oracle figure
 CPU_SAMPLED = ("cpu-plumbing", "qwen3-8b-single", "qwen3-8b-ragged", "llama31-8b-ctx32k-p128",
                "qwen3-8b-stress-b32")
@@ -596,7 +596,7 @@ def attn_workload(dev, name, steps, warmup, cpu=False):
     import torch
     from cast_amd import scenarios
     if name.endswith(("-fp32", "-fp16")):
-        # the headline shapes in fp32 (what the unchanged reference hook hands
+        # a workload's shapes in fp32 (what the unchanged reference hook hands
         # the kernel, cast_trees/serving.py:68-71) or in fp16 (same MFMA rate
         # as bf16 on this part)
         wl = dataclasses.replace(scenarios.CONFIGS[name[:-5]](), dtype=name[-4:], name=name)

@@ -1115,8 +1115,8 @@ void tree_attn_mfma_kernel(AttnArgs a) {
     }
 }
 // --------------------------------------------------------------------------
-// MFMA kernel for fp32 inputs: head_dim D in {64, 128}, WAVES waves x 32
-// query rows, v_mfma_f32_32x32x2_f32.  The reference hook runs its kernel on
+// MFMA kernel for fp32 inputs: head_dim D in {64, 128, 256}, WAVES waves x
+// 32 query rows, v_mfma_f32_32x32x2_f32.  The reference hook runs its kernel on
 // fp32 copies of q/k/v (cast_trees/serving.py:68-71), where p stays fp32
 // for the value product (tree_attn.py:66,87 cast p to the input dtype):
 // so does this kernel.  Same structure as the bf16 kernel: S^T = K Q^T with
@@ -1131,15 +1131,19 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 // output blocks.  The product is MFMA-bound (16 x the bf16 cycles per
 // flop): staging and softmax are small beside it.
 // --------------------------------------------------------------------------
+// Key tiles hold 64 keys (two 32-key blocks), or 32 at head dim 256, where
+// two double-buffered 64-key K and V' tiles would not fit in LDS.
 // WPE: waves per SIMD the register budget is sized for: 2, except the
-// 4-wave head_dim-128 instance (1): its threads each stage twice the 8-wave
-// instance's share of a tile, and its 135 KB of LDS leave room for one
-// workgroup (one wave per SIMD) per CU anyway.
+// 4-wave head-dim-128 and -256 instances (1): the former's threads each
+// stage twice the 8-wave instance's share of a tile, the latter holds 128
+// registers of Q and 128 of O per lane; their 133-135 KB of LDS leave room
+// for one workgroup (one wave per SIMD) per CU anyway.
 template <int D, int WAVES, bool STORE, int WPE = 2, bool SKI = false>
 __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void tree_attn_f32_kernel(AttnArgs a) {
     constexpr int NT = WAVES * 64;
-    constexpr int BN = 64;                 // keys per tile
+    constexpr int BN = D <= 128 ? 64 : 32;  // keys per tile
+    constexpr int NKB = BN / 32;           // 32-key MFMA blocks per tile
     constexpr int ROWS = WAVES * 32;       // query rows per workgroup
     constexpr int DH = D / 2;              // k-steps per 32-key block (2 head-dim values each)
     constexpr int DB = D / 32;             // 32-row blocks of O^T
@@ -1315,14 +1319,15 @@ void tree_attn_f32_kernel(AttnArgs a) {
         const bool pack_tile = t >= n_pre;
         // in a pack tile, the 32-key blocks no row of the wave sees are
         // skipped: scores -inf, no PV product
-        bool live[2] = {true, true};
-        if (!SKI && pack_tile) {
-            live[0] = block_live(mw0, mw1, t0 - sq.S, valid);
-            live[1] = block_live(mw0, mw1, t0 - sq.S + 32, valid - 32);
-        }
+        bool live[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+            live[kb] = SKI || !pack_tile || block_live(mw0, mw1, t0 - sq.S + 32 * kb, valid - 32 * kb);
         // S^T = K Q^T, the two 32-key blocks' chains interleaved
-        floatx16 s[2] = {floatx16{}, floatx16{}};
-        if (live[0] && live[1]) {
+        floatx16 s[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) s[kb] = floatx16{};
+        if (NKB == 2 && live[0] && live[NKB - 1]) {
 #pragma unroll
             for (int i = 0; i < DH / 4; ++i) {
                 const floatx4 k0 = *reinterpret_cast<const floatx4 *>(&Ks[buf][l32 * KPAD + DH * g + 4 * i]);
@@ -1330,12 +1335,12 @@ void tree_attn_f32_kernel(AttnArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0[j], qf[4 * i + j], s[0], 0, 0, 0);
-                    s[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1[j], qf[4 * i + j], s[1], 0, 0, 0);
+                    s[NKB - 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1[j], qf[4 * i + j], s[NKB - 1], 0, 0, 0);
                 }
             }
         } else {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
                 if (!live[kb]) {
 #pragma unroll
                     for (int e = 0; e < 16; ++e) s[kb][e] = -INFINITY;
@@ -1353,7 +1358,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
         // visibility on pack tiles and partial tiles (as in the bf16 kernel)
         if (pack_tile || valid < BN) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < NKB; ++kb) {
                 const int k0 = kb * 32 + 4 * g;
                 const int lim = valid - k0;
                 uint32_t vis = pack_tile ? vis_window(mw0, mw1, t0 - sq.S + k0) : ~0u;
@@ -1369,7 +1374,9 @@ void tree_attn_f32_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 1; e < 16; ++e) lmax = fmaxf(lmax, s[0][e]);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) lmax = fmaxf(lmax, s[1][e]);
+        for (int kb = 1; kb < NKB; ++kb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) lmax = fmaxf(lmax, s[kb][e]);
         if (__any(lmax * c > m + kRescaleSlack)) {
             const float mx = fmaxf(lmax, partner32(lmax)) * c;
             const float mn = fmaxf(m, mx);
@@ -1382,7 +1389,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
         }
         float acc = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 s[kb][e] = __builtin_amdgcn_exp2f(fmaf(s[kb][e], c, -msafe));
@@ -1391,7 +1398,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
         lsum += acc;
         // O^T += V^T P^T: step e of block kb is key 32*kb + 8*(e/4) + 4*g + e%4
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
             if (!live[kb]) continue;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -1854,7 +1861,7 @@ static Topology device_topology() {
 }
 
 static bool mfma_path(int32_t dtype, int32_t D) {
-    if (dtype == CAST_FP32) return D == 64 || D == 128;
+    if (dtype == CAST_FP32) return D == 64 || D == 128 || D == 256;
     return (dtype == CAST_BF16 || dtype == CAST_FP16) && (D == 64 || D == 128 || D == 256);
 }
 
@@ -1936,11 +1943,13 @@ static AttnKernel attn_kernel_of(int32_t dtype, int32_t D, int waves, bool store
     return waves == 4 ? mfma_instance<64, 4, 2, SKI>(f16, store) : mfma_instance<64, 8, 2, SKI>(f16, store);
 }
 // Head dims 64 and 128 run 2, 4 or 8 waves (bf16 / fp16) or 4 or 8 (fp32);
-// head dim 256 runs 4 (bf16 / fp16, static schedule only).  WPE (waves per
+// head dim 256 runs 4 (static schedule only).  WPE (waves per
 // SIMD of the register budget) as the kernels' comments give it; sk picks
 // the stream-K instance.
 static AttnKernel attn_kernel(int32_t dtype, int32_t D, int waves, bool store, bool sk) {
-    if (D == 256) return mfma_instance<256, 4, 1, false>(dtype == CAST_FP16, store);
+    if (D == 256)
+        return dtype == CAST_FP32 ? f32_instance<256, 4, 1, false>(store)
+                                  : mfma_instance<256, 4, 1, false>(dtype == CAST_FP16, store);
     return sk ? attn_kernel_of<true>(dtype, D, waves, store) : attn_kernel_of<false>(dtype, D, waves, store);
 }
 
@@ -2174,7 +2183,8 @@ static int tree_attn_run(const void *q, const KvSource &kv, void *out, float *ls
     (a.sk_mode ? tree_attn_combine_kernel<OT, DD, E, true><<<cg, 256, 0, st>>>(a) \
                : tree_attn_combine_kernel<OT, DD, E, false><<<cg, 256, 0, st>>>(a))
         if (dtype == CAST_FP32) {
-            if (head_dim == 128) CAST_COMBINE(float, 128, Bf16);
+            if (head_dim == 256) tree_attn_combine_kernel<float, 256, Bf16, false><<<cg, 256, 0, st>>>(a);
+            else if (head_dim == 128) CAST_COMBINE(float, 128, Bf16);
             else CAST_COMBINE(float, 64, Bf16);
         } else if (dtype == CAST_FP16) {
             if (head_dim == 256) tree_attn_combine_kernel<uint16_t, 256, Fp16, false><<<cg, 256, 0, st>>>(a);

@@ -93,9 +93,9 @@ int cast_tree_bitmask(const int32_t *parent, const int32_t *cu_q, int32_t batch,
  *   mask   uint64 [total_q][mask_words], mask_words 1 (int64 reference
  *          layout) or 2
  *   dtype  cast_dtype of q, k, v and out: CAST_BF16, CAST_FP16 or CAST_FP32
- *   head_dim  64 or 128 on the MFMA kernels (bf16 and fp16 also 256); any
- *          other multiple of 8 up to 256 on a scalar kernel (the reference
- *          takes any power of two)
+ *   head_dim  64, 128 or 256 on the MFMA kernels; any other multiple of 8
+ *          up to 256 on a scalar kernel (the reference takes any power of
+ *          two)
  *   sm_scale  > 0 (the Python layer substitutes 1/sqrt(D) for None)
  *   kv_split  keys per split-K chunk (multiple of 64); 0 lets the library
  *             choose; CAST_SPLIT_STREAM (-2) asks for the stream-K schedule;

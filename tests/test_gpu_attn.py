@@ -145,14 +145,14 @@ def test_fp16_inputs(gpu):
 
 def test_head_dims_above_128(gpu):
     # the reference kernel takes any power-of-two head_dim (tl.arange(0, D),
-    # tree_attn.py:36): 256 in bf16/fp16 runs the MFMA kernel at one wave per
-    # SIMD; fp32 at 256 and the other multiples of 8 take the scalar kernel
+    # tree_attn.py:36): 256 runs the MFMA kernels at one wave per SIMD (bf16,
+    # fp16 and fp32); the other multiples of 8 take the scalar kernel
     for Hq, Hkv, D, dt in [(8, 2, 256, "bf16"), (4, 4, 256, "fp32"), (8, 4, 192, "bf16"), (4, 1, 136, "fp32")]:
         wl = SC.random_parent_batch(seed=D + Hq, B=3, Hq=Hq, Hkv=Hkv, D=D, s_lo=20, s_hi=300, p_lo=1, p_hi=129,
                                     dtype=dt, qkv_scale=0.5)
         _run_and_check(wl, gpu, label=f"head-dim-{D}-{Hq}/{Hkv}-{dt}")
-    # head_dim 256 on MFMA: long prefixes, split-K and the combine, both formats
-    for dt in ("bf16", "fp16"):
+    # head_dim 256 on MFMA: long prefixes, split-K and the combine, every format
+    for dt in ("bf16", "fp16", "fp32"):
         wl = SC.random_parent_batch(seed=7, B=4, Hq=16, Hkv=8, D=256, s_lo=500, s_hi=4000, p_lo=1, p_hi=129,
                                     dtype=dt, qkv_scale=0.5)
         for split in (0, 256, -1):
@@ -475,3 +475,17 @@ def test_arbitrary_visibility_words(gpu, dtype, kv_split):
                 words[q0 + i, j >> 6] |= np.uint64(1) << np.uint64(j & 63)
     print(f"case arbitrary-words {dtype} split={kv_split}: B={wl.B} total_q={wl.total_q}", flush=True)
     _run_and_check(wl, gpu, kv_split=kv_split, words=words, label=f"arbitrary-words-{dtype}-{kv_split}")
+
+
+def test_fp32_head_dim_256_edges(gpu):
+    # fp32 at head dim 256: 32-key tiles (one MFMA block a tile), the tree
+    # block alone, a single root, chains and stars, the one-word mask, and
+    # packs whose pack tiles no row of a workgroup sees past some key
+    import dataclasses
+    wl = dataclasses.replace(_edges("fp32"), Hq=8, Hkv=4, D=256, qkv_scale=0.5)
+    for split in (0, 128):
+        _run_and_check(wl, gpu, kv_split=split, label=f"fp32-d256-edges-split{split}")
+    wl = SC.random_parent_batch(seed=31, B=4, Hq=8, Hkv=2, D=256, s_lo=0, s_hi=200, p_lo=1, p_hi=65,
+                                dtype="fp32", qkv_scale=0.5)
+    for split in (0, 64):
+        _run_and_check(wl, gpu, kv_split=split, one_word=True, label=f"fp32-d256-one-word-split{split}")

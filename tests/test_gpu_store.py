@@ -90,8 +90,8 @@ def test_store_head_dim_64_and_large_batches(gpu, dtype, B, kv_split):
 
 
 def test_store_head_dim_256(gpu):
-    # head_dim 256 (the MFMA kernel at one wave per SIMD) reading the store in place
-    for dt, split in (("bf16", 0), ("fp16", 192)):
+    # head_dim 256 (the MFMA kernels at one wave per SIMD) reading the store in place
+    for dt, split in (("bf16", 0), ("fp16", 192), ("fp32", 0), ("fp32", 96)):
         wl = SC.random_parent_batch(seed=11, B=3, Hq=8, Hkv=4, D=256, s_lo=100, s_hi=2000, p_lo=1, p_hi=129,
                                     dtype=dt, qkv_scale=0.5)
         _check_store(wl, gpu, kv_split=split, label=f"store-d256-{dt}-split{split}")
