@@ -1126,9 +1126,12 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 // (D/2)*g + step of its key and of its query, so a lane's K operands for
 // four steps are one 16-byte LDS read; in the PV product it supplies the
 // value of key 8*(e/4) + 4*g + e%4 at step e, which is exactly its own
-// accumulator element e.  V sits in LDS as V'[key][l*DB + db] =
+// accumulator element e.  V sits in LDS as V'[key][vpos(l)*DB + db] =
 // V[key][32*db + l], so one read gives lane l the operands of all DB
-// output blocks.  The product is MFMA-bound (16 x the bf16 cycles per
+// output blocks; vpos(l) = 8*(l%4) + l/4 (a 4x8 transpose of the group
+// index) puts the eight groups of a key that one staging store covers
+// (l = 4*lg + i, lg = 0..7) side by side, on distinct banks; the reads
+// take a permutation of the same row.  The product is MFMA-bound (16 x the bf16 cycles per
 // flop): staging and softmax are small beside it.
 // --------------------------------------------------------------------------
 // Key tiles hold 64 keys (two 32-key blocks), or 32 at head dim 256, where
@@ -1245,7 +1248,8 @@ void tree_attn_f32_kernel(AttnArgs a) {
                 vst[it][db] = load16(vrs, __umul24(row0 + key, vsb) + db * 128 + lg * 16);
         }
     };
-    // register -> LDS: K as is; V with d = 32*db + l stored at l*DB + db
+    // register -> LDS: K as is; V with d = 32*db + l stored at vpos(l)*DB + db
+    auto vpos = [](int l) __attribute__((always_inline)) { return 8 * (l & 3) + (l >> 2); };
     auto publish = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int it = 0; it < K_PER_T; ++it) {
@@ -1269,7 +1273,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
                     const uint32_t bits = vst[it][db][i];
                     w[db] = __builtin_bit_cast(float, bits);
                 }
-                *reinterpret_cast<floatxDB *>(&Vs[buf][key * KPAD + (4 * lg + i) * DB]) = w;
+                *reinterpret_cast<floatxDB *>(&Vs[buf][key * KPAD + vpos(4 * lg + i) * DB]) = w;
             }
         }
     };
@@ -1403,7 +1407,7 @@ void tree_attn_f32_kernel(AttnArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int key = kb * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-                const floatxDB vv = *reinterpret_cast<const floatxDB *>(&Vs[buf][key * KPAD + l32 * DB]);
+                const floatxDB vv = *reinterpret_cast<const floatxDB *>(&Vs[buf][key * KPAD + vpos(l32) * DB]);
 #pragma unroll
                 for (int db = 0; db < DB; ++db)
                     o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[db], s[kb][e], o[db], 0, 0, 0);
