@@ -17,11 +17,14 @@
 //   O^T += V^T P^T with the same instruction, P^T taken straight from the
 //   S^T accumulator registers (a lane's 16 score values are exactly the 8+8
 //   k-slots it must supply), V^T read from a transposed LDS copy.  fp32
-//   inputs run the same structure on v_mfma_f32_32x32x2_f32
-//   (tree_attn_f32_kernel); other head dims (up to 256) take a scalar
-//   kernel.  Head_dim 256 runs one wave per SIMD (512 registers a lane).
-// K/V tiles of 64 keys are double-buffered through LDS with 16-byte loads;
-// the ancestor words are only consulted on the tile(s) holding pack keys.
+//   inputs with head_dim 64/128/256 run the same structure on
+//   v_mfma_f32_32x32x2_f32 (tree_attn_f32_kernel); other head dims (up to
+//   256) take a scalar kernel.  Head_dim 256 runs one wave per SIMD (512
+//   registers a lane).
+// K/V tiles of 64 keys (32 for fp32 at head_dim 256) are double-buffered
+// through LDS with 16-byte loads; the ancestor words are only consulted on
+// the tile(s) holding pack keys, and pack tiles past the last key any row
+// of a workgroup sees are skipped.
 // The online softmax works in base 2 with a lazy rescale: the running max
 // moves only when a tile raises it by more than 2^8, so most tiles skip the
 // O rescale.  Every workgroup decodes its unit from the device-side metadata
