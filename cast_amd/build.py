@@ -66,7 +66,9 @@ def bench_sources():
 
 # warnings that fail the build: a kernel that misses its occupancy target
 # runs with fewer waves than its tiling assumes
-_FATAL = ("failed to meet occupancy target",)
+# a kernel that misses its amdgpu_waves_per_eu target, or any other pass the
+# compiler was asked to apply and could not (an unroll pragma, for one)
+_FATAL = ("failed to meet occupancy target", "-Wpass-failed")
 
 
 def _compile(hipcc, src, objdir, inc):
@@ -118,7 +120,8 @@ def build(verbose: bool = True) -> Path:
         if any(f in text for f in _FATAL):
             fatal.append(src.name)
     if fatal:
-        raise RuntimeError(f"a kernel misses its occupancy target (amdgpu_waves_per_eu) in {', '.join(fatal)}")
+        raise RuntimeError("a kernel misses its occupancy target (amdgpu_waves_per_eu) or a requested "
+                           f"optimisation (-Wpass-failed) in {', '.join(fatal)}")
     n = len(sources())
     _link(hipcc, [o for _, o, _ in done[:n]], OUT)
     _link(hipcc, [o for _, o, _ in done[n:]], BENCH_OUT)
