@@ -617,9 +617,9 @@ __device__ bool sk_next_segment(const AttnArgs &a, WorkCursor &cur, Unit &u, con
 // The first piece of work of the calling workgroup, after the batch
 // prologue; false when it has none (or the batch was rejected).  Batches of
 // up to 64 requests take the stream-K lanes when the caller asked for them
-// and sk_plan accepts the batch, else the longest-first schedule; larger ones take items in batch order,
-// consecutive items (the row blocks of one key split) on one XCD so that
-// they share its L2.  skr: LDS for the stream-K table (64 entries).
+// and sk_plan accepts the batch, else the longest-first schedule; larger
+// ones take items in batch order, consecutive items (the row blocks of one
+// key split) on one XCD so that they share its L2.  skr: LDS for the stream-K table (64 entries).
 template <bool SK>   // SK: the kernel instance takes the stream-K schedule when the plan asks
 __device__ bool first_unit(const AttnArgs &a, WorkCursor &cur, Unit &u, SkReq *skr) {
     cur.sk = false;
@@ -1134,8 +1134,8 @@ void tree_attn_mfma_kernel(AttnArgs a) {
 // output blocks; vpos(l) = 8*(l%4) + l/4 (a 4x8 transpose of the group
 // index) puts the eight groups of a key that one staging store covers
 // (l = 4*lg + i, lg = 0..7) side by side, on distinct banks; the reads
-// take a permutation of the same row.  The product is MFMA-bound (16 x the bf16 cycles per
-// flop): staging and softmax are small beside it.
+// take a permutation of the same row.  The product is MFMA-bound (16 x the
+// bf16 cycles per flop): staging and softmax are small beside it.
 // --------------------------------------------------------------------------
 // Key tiles hold 64 keys (two 32-key blocks), or 32 at head dim 256, where
 // two double-buffered 64-key K and V' tiles would not fit in LDS.
@@ -1338,7 +1338,8 @@ void tree_attn_f32_kernel(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < DH / 4; ++i) {
                 const floatx4 k0 = *reinterpret_cast<const floatx4 *>(&Ks[buf][l32 * KPAD + DH * g + 4 * i]);
-                const floatx4 k1 = *reinterpret_cast<const floatx4 *>(&Ks[buf][(32 + l32) * KPAD + DH * g + 4 * i]);
+                const floatx4 k1 =
+                    *reinterpret_cast<const floatx4 *>(&Ks[buf][((NKB - 1) * 32 + l32) * KPAD + DH * g + 4 * i]);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     s[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0[j], qf[4 * i + j], s[0], 0, 0, 0);
@@ -1355,7 +1356,8 @@ void tree_attn_f32_kernel(AttnArgs a) {
                 }
 #pragma unroll
                 for (int i = 0; i < DH / 4; ++i) {
-                    const floatx4 kk = *reinterpret_cast<const floatx4 *>(&Ks[buf][(kb * 32 + l32) * KPAD + DH * g + 4 * i]);
+                    const floatx4 kk =
+                        *reinterpret_cast<const floatx4 *>(&Ks[buf][(kb * 32 + l32) * KPAD + DH * g + 4 * i]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
                         s[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[j], qf[4 * i + j], s[kb], 0, 0, 0);
