@@ -97,25 +97,27 @@ def test_store_head_dim_256(gpu):
         _check_store(wl, gpu, kv_split=split, label=f"store-d256-{dt}-split{split}")
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(64))
 def test_random_configurations(gpu, seed):
     # seeded random shapes across features the other tests take one at a time:
     # batches past 64 requests, GQA ratios down to one KV head, head dims on
-    # the MFMA and scalar kernels, the three element types, split-K settings;
-    # both K/V layouts, bit-identical to each other, and sampled requests
-    # against the oracle
+    # the MFMA and scalar kernels, the three element types, split-K settings
+    # (stream-K included), short and long packs (trimmed pack tiles); both
+    # K/V layouts, bit-identical to each other, and sampled requests against
+    # the oracle
     rng = np.random.default_rng(1000 + seed)
     Hkv, G = int(rng.choice([1, 2, 4, 8])), int(rng.choice([1, 2, 4, 8]))
     D = int(rng.choice([64, 96, 128, 256]))
     dt = str(rng.choice(["bf16", "fp16", "fp32"]))
-    B = int(rng.choice([1, 3, 8, 40, 70]))
-    s_hi = int(rng.choice([2, 300, 2500]))
-    split = int(rng.choice([0, 64, 320, -1, -2]))
-    wl = SC.random_parent_batch(seed=seed, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, s_lo=0, s_hi=s_hi, p_lo=1, p_hi=129,
+    B = int(rng.choice([1, 3, 8, 17, 40, 70]))
+    s_hi = int(rng.choice([2, 300, 2500, 5000]))
+    p_hi = int(rng.choice([17, 65, 129]))
+    split = int(rng.choice([0, 64, 128, 320, -1, -2]))
+    wl = SC.random_parent_batch(seed=seed, B=B, Hq=Hkv * G, Hkv=Hkv, D=D, s_lo=0, s_hi=s_hi, p_lo=1, p_hi=p_hi,
                                 dtype=dt, qkv_scale=0.5)
     requests = sorted(rng.choice(B, size=min(B, 3), replace=False).tolist())
     _check_store(wl, gpu, kv_split=split, requests=requests,
-                 label=f"random-{seed}: Hq={Hkv * G} Hkv={Hkv} D={D} {dt} B={B} S<{s_hi} split={split}")
+                 label=f"random-{seed}: Hq={Hkv * G} Hkv={Hkv} D={D} {dt} B={B} S<{s_hi} P<{p_hi} split={split}")
 
 
 def test_store_empty_and_tiny_prefixes(gpu):
