@@ -290,3 +290,21 @@ def test_head_dim_bounds(lib):
     ptrs = dict(q=fake, k=fake, v=fake, out=fake, cu_q=fake, cu_kv=fake, prefix=fake, pack=fake, mask=fake)
     for D in (264, 100, 4, 512):
         assert _attn(lib, D=D, **ptrs) == 5, D
+
+
+def test_build_fails_on_occupancy_and_pass_failed_warnings():
+    # cast_amd.build stops on a kernel that misses its waves-per-SIMD target or
+    # on any other -Wpass-failed warning, and drops only hipcc's note that the
+    # host pass does not know the device-only packed-fp32 feature
+    from cast_amd import build as B
+    host_note = "warning: '-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
+    assert B._warnings(host_note) == ""
+    occ = ("tree_attn.hip:700:1: warning: void cast::k(): failed to meet occupancy target given by "
+           "'amdgpu-waves-per-eu' in 'k': desired occupancy was 2, final occupancy is 1 [-Wpass-failed]")
+    unroll = "draft.hip:10:5: warning: loop not unrolled: the optimizer was unable to perform the " \
+             "requested transformation [-Wpass-failed=transform-warning]"
+    other = "store.hip:3:1: warning: unused variable 'x' [-Wunused-variable]"
+    for text, fatal in ((occ, True), (unroll, True), (other, False)):
+        kept = B._warnings(host_note + "\n" + text)
+        assert kept == text
+        assert any(f in kept for f in B._FATAL) == fatal
