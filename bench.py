@@ -624,19 +624,38 @@ def attn_workload(dev, name, steps, warmup, cpu=False):
 
 def secondary(dev, steps, warmup, cpu=True):
     """Every other workload, each entry with the timed and untimed call
-    counts it used."""
+    counts it used.  A workload that raises is recorded with its error, so
+    that it cannot take the headline line down with it."""
+    import torch
     res = {}
+
+    def guarded(key, fn):
+        try:
+            return fn()
+        except Exception as e:   # noqa: BLE001  (reported in the line, not swallowed)
+            log(f"  {key}: FAILED {type(e).__name__}: {e}")
+            try:   # release what the failed workload held before the next one
+                torch.cuda.synchronize()
+                torch.cuda.empty_cache()
+            except Exception:   # noqa: BLE001
+                pass
+            return dict(error=f"{type(e).__name__}: {e}")
+
     for name in ATTN_WORKLOADS:
-        res[name] = attn_workload(dev, name, steps, warmup, cpu=cpu and name in CPU_SAMPLED)
+        res[name] = guarded(name, lambda: attn_workload(dev, name, steps, warmup, cpu=cpu and name in CPU_SAMPLED))
     # fresh stores settle over ~20 calls
     runs = [("store_layout", store_layout, max(steps, 60), max(warmup, 20)),
             ("kv_append", kv_append, steps, warmup), ("cache_gather", cache_gather, steps, warmup),
             ("draft_trees", draft_trees, steps, warmup), ("graph_replay", graph_replay, steps, warmup),
             ("verify_round", verify_round, steps, warmup)]
     for key, fn, n, w in runs:
-        res[key] = dict(fn(dev, n, w), steps=n, warmup=w)
-    for key, r in bitmask_lines(dev, steps, warmup).items():
-        res[key] = dict(r, steps=steps, warmup=warmup)
+        res[key] = guarded(key, lambda: dict(fn(dev, n, w), steps=n, warmup=w))
+    lines = guarded("tree_bitmask", lambda: bitmask_lines(dev, steps, warmup))
+    if "error" in lines:
+        res["tree_bitmask"] = lines
+    else:
+        for key, r in lines.items():
+            res[key] = dict(r, steps=steps, warmup=warmup)
     return res
 
 

@@ -50,3 +50,21 @@ def test_cpu_sample_scales_by_score_count():
     rg = SC.random_parent_batch(seed=3, B=4, Hq=4, Hkv=2, D=64, s_lo=32, s_hi=96, p_lo=4, p_hi=16)
     r = bench.cpu_baseline_sample(rg, budget_s=0.2)
     assert r["value"] > 0 and "of 4" in r["sample"]
+
+
+def test_a_failing_secondary_workload_is_recorded_not_fatal(monkeypatch):
+    # every secondary workload replaced by a fake (no device work); one raises
+    def fake_attn(dev, name, steps, warmup, cpu=False):
+        if name == "qwen3-8b-ragged":
+            raise RuntimeError("planted failure")
+        return dict(us_per_call=1.0, steps=steps, warmup=warmup)
+
+    monkeypatch.setattr(bench, "attn_workload", fake_attn)
+    for fn in ("store_layout", "kv_append", "cache_gather", "draft_trees", "graph_replay", "verify_round"):
+        monkeypatch.setattr(bench, fn, lambda dev, n, w: dict(ok=1))
+    monkeypatch.setattr(bench, "bitmask_lines", lambda dev, n, w: {"tree_bitmask": dict(us_per_call=1.0)})
+    res = bench.secondary(None, 50, 20, cpu=False)
+    assert res["qwen3-8b-ragged"] == {"error": "RuntimeError: planted failure"}
+    assert res["qwen3-8b-single"]["us_per_call"] == 1.0
+    assert res["verify_round"] == {"ok": 1, "steps": 50, "warmup": 20}
+    assert res["tree_bitmask"]["steps"] == 50
